@@ -1,0 +1,117 @@
+// Host-side launchers for the HIP kernels.  Every launcher enqueues on the
+// given stream and returns 0 or a status code; none of them synchronizes.
+#pragma once
+#include "sq_common.h"
+
+namespace sq {
+
+// ---- decode matvec (k_gemv.hip) -------------------------------------------
+enum GemvPro : int {
+    PRO_NORM = 0,  // RMSNorm(x) * norm_w computed in every workgroup, then
+                   // quantized (A8) or kept f32 (A32) in LDS
+    PRO_Q8 = 1,    // quantized activation blocks read from global memory
+    PRO_F32 = 2,   // f32 activations read from global memory
+};
+enum GemvEpi : int {
+    EPI_STORE = 0,   // out[row] = v
+    EPI_QKV = 1,     // RoPE on q/k rows, q -> q_out, k/v -> cache row `pos`
+    EPI_RESID = 2,   // out[row] += v  (residual add into hidden)
+    EPI_GATEUP = 3,  // silu(gate)*up -> ffn_act (+ Q8_0 blocks)
+    EPI_LOGITS = 4,  // logits[row] = v, per-workgroup argmax partials
+};
+
+struct GemvArgs {
+    MatView w;
+    int n_rows;        // logical output rows (EPI_GATEUP: ffn width)
+    // prologue inputs
+    const float* x;        // PRO_NORM / PRO_F32
+    const float* norm_w;   // PRO_NORM
+    float eps;
+    const int8_t* aq;      // PRO_Q8: activation payload [k]
+    const uint16_t* ad;    // PRO_Q8: activation scales [k/32]
+    // epilogue outputs
+    float* out;
+    float* q_out;          // EPI_QKV
+    float* kcache;
+    float* vcache;
+    const float2* rope;    // [max_pos][head_dim/2] (cos, sin)
+    const int* pos;        // device position counter
+    int q_rows, kv_rows, half;
+    float* ffn_act;        // EPI_GATEUP
+    int8_t* act_q;
+    uint16_t* act_d;
+    float* part_val;       // EPI_LOGITS
+    int* part_idx;
+    int* part_nan;
+    // debug taps of the prologue (workgroup 0 only, when non-null)
+    float* dbg_normed;
+    int8_t* dbg_qs;
+    uint16_t* dbg_d;
+};
+
+// a8: quantized activations (false: f32 activations).  Returns the number of
+// workgroups launched through *grid_out when not null.
+int launch_gemv(hipStream_t s, int pro, int epi, bool a8, const GemvArgs& a, int* grid_out);
+
+// ---- attention (k_attn.hip) ------------------------------------------------
+// Decode: one query row per head at position *pos, keys 0..*pos (inclusive).
+int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const float* vcache,
+                       const int* pos, int n_heads, int n_kv_heads, int head_dim, int nsplit,
+                       float* part_m, float* part_l, float* part_o);
+// Merge the split partials; writes attn f32 and, when act_q != null, Q8_0
+// blocks of each head's output (the o-projection's quantized input).
+int launch_attn_combine(hipStream_t s, const float* part_m, const float* part_l,
+                        const float* part_o, int n_heads, int head_dim, int nsplit, float* attn,
+                        int8_t* act_q, uint16_t* act_d);
+// Prefill: m query rows at positions pos0 .. pos0+m-1 against keys 0..pos0+m-1.
+int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, const float* vcache,
+                        int pos0, int m, int n_heads, int n_kv_heads, int head_dim,
+                        float* out);
+// Any head_dim: one wavefront per (query, head) row; op-level entry point.
+int launch_sdpa_generic(hipStream_t s, const float* q, const float* k, const float* v, float* out,
+                        int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim);
+
+// ---- row kernels (k_misc.hip) -------------------------------------------
+int launch_embed(hipStream_t s, const MatView& table, int wtype, const uint32_t* tokens,
+                 int n_tokens, int dim, float* out);
+int launch_rmsnorm_rows(hipStream_t s, const float* x, const float* w, int rows, int dim,
+                        float eps, float* out, int8_t* act_q, uint16_t* act_d);
+int launch_quantize_rows(hipStream_t s, const float* x, size_t n, int8_t* qs, uint16_t* d);
+int launch_pack_q8_blocks(hipStream_t s, const int8_t* qs, const uint16_t* d, size_t nblocks,
+                          void* gguf_blocks);
+int launch_unpack_q8_blocks(hipStream_t s, const void* gguf_blocks, size_t nblocks, int8_t* qs,
+                            uint16_t* d);
+// Row m of qkv ([m][ld], q | k | v) is at position pos0 + m: q is rotated into
+// q_out [m][q_dim], k rotated and v copied into cache row pos0 + m.
+int launch_rope_kv_rows(hipStream_t s, const float* qkv, int ld, int rows, int q_dim, int kv_dim,
+                        int head_dim, int pos0, const float2* rope, float* q_out, float* kcache,
+                        float* vcache);
+int launch_rope_rows_table(hipStream_t s, float* t, int rows, int row_dim, int head_dim,
+                           const float2* cs_rows);
+// gu holds [gate | up] rows of 2*ffn; writes silu(gate)*up for n = rows*ffn
+// values (and their Q8_0 blocks when act_q is non-null).
+int launch_silu_mul_rows(hipStream_t s, const float* gu, int ffn, size_t n, float* out,
+                         int8_t* act_q, uint16_t* act_d);
+int launch_silu(hipStream_t s, float* x, size_t n);
+int launch_mul(hipStream_t s, const float* a, const float* b, float* out, size_t n);
+int launch_add_inplace(hipStream_t s, float* a, const float* b, size_t n);
+int launch_softmax_row(hipStream_t s, const float* in, float* out, int n);
+// Final argmax over the LM head partials (or a full scan when a NaN was
+// seen); writes token[0], appends to history[*pos_hist] when history is
+// non-null, and advances *pos by `advance`.
+int launch_argmax_final(hipStream_t s, const float* logits, int n, const float* part_val,
+                        const int* part_idx, const int* part_nan, int n_parts, uint32_t* token,
+                        int* pos, int advance, uint32_t* history, int* n_hist);
+int launch_argmax_partials(hipStream_t s, const float* logits, int n, float* part_val,
+                           int* part_idx, int* part_nan, int n_parts);
+int launch_block_isums(hipStream_t s, const int8_t* aq, const MatView& w, int wtype, int row,
+                       int32_t* out);
+int launch_copy_i32(hipStream_t s, const int* src, int* dst);
+
+// ---- prefill matmul (k_gemm.hip) ----------------------------------------
+// out[m, rows] (+)= in[m, k] @ W.  a8: activations given as Q8_0 (aq/ad,
+// [m][k] / [m][k/32]); otherwise f32 activations x [m][k].
+int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq,
+                const uint16_t* ad, const float* x, int m, float* out, int ldo, bool accumulate);
+
+}  // namespace sq

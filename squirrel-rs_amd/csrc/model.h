@@ -1,0 +1,131 @@
+// Llama model and inference context on one GPU.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "gguf.h"
+#include "launch.h"
+
+namespace sq {
+
+// LlamaConfig (src/models/llama/config.rs:10-26).
+struct Config {
+    int n_layers = 0, dim = 0, ffn = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, vocab = 0;
+    int context_length = 0;
+    uint32_t bos = 0, eos = 0;
+    float rope_base = 0.f, eps = 0.f;
+    std::vector<float> inv_freq;  // head_dim / 2
+};
+
+// LlamaConfig::from_gguf (config.rs:29-73) incl. compute_rope_inv_freq
+// (config.rs:83-127).  SQ_ERR_CONFIG on MissingMetadata / WrongMetadataType.
+int read_config(const GGUFFile& f, Config* cfg);
+void rope_inv_freq(int head_dim, float base, float factor, float low, float high, float orig_ctx,
+                   float* out);
+
+// Upload `rows` rows of GGUF blocks into the device layout (DevMatrix).
+int upload_matrix(int wtype, const uint8_t* blocks, size_t rows, size_t k, DevMatrix* out);
+// Upload several GGUF matrices with equal k as one stacked device matrix.
+int upload_stacked(int wtype, const std::vector<const uint8_t*>& parts,
+                   const std::vector<size_t>& rows, size_t k, DevMatrix* out);
+void free_matrix(DevMatrix* m);
+
+struct Layer {
+    float* attn_norm = nullptr;
+    DevMatrix qkv;     // [q rows; k rows; v rows]
+    DevMatrix o;
+    float* ffn_norm = nullptr;
+    DevMatrix gateup;  // [gate rows; up rows]
+    DevMatrix down;
+};
+
+}  // namespace sq
+
+struct sq_model {
+    sq::Config cfg;
+    int wtype = 0;
+    bool tied = true;
+    std::vector<sq::Layer> layers;
+    sq::DevMatrix embd;     // token_embd rows: the embedding table
+    sq::DevMatrix head;     // LM head rows (aliases embd when tied)
+    float* out_norm = nullptr;
+    uint64_t weight_bytes = 0;
+    int device = 0;
+};
+
+struct sq_ctx {
+    const sq_model* m = nullptr;
+    hipStream_t stream = nullptr;
+    size_t max_pos = 0;
+    uint32_t flags = 0;
+    bool a8 = true;           // quantized activations on the matvecs
+    size_t seq_len = 0;       // host mirror of *d_pos
+
+    float* kcache = nullptr;  // [layer][max_pos][kv_dim]
+    float* vcache = nullptr;
+    float2* rope = nullptr;   // [max_pos][head_dim/2] (cos, sin)
+    int* d_pos = nullptr;
+    uint32_t* d_token = nullptr;
+    uint32_t* d_ids = nullptr;   // prompt ids [max_pos]
+    uint32_t* d_hist = nullptr;  // generated ids [max_pos]
+    int* d_nhist = nullptr;
+
+    // decode workspace
+    float* hidden = nullptr;
+    float* q = nullptr;
+    float* attn = nullptr;
+    int8_t* attn_q = nullptr;
+    uint16_t* attn_d = nullptr;
+    float* ffn_act = nullptr;
+    int8_t* ffn_q = nullptr;
+    uint16_t* ffn_d = nullptr;
+    float* logits = nullptr;
+    float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
+    int nsplit = 0;
+    float* pv = nullptr;
+    int* pi = nullptr;
+    int* pn = nullptr;
+    int n_parts = 0;
+    float* dbg_normed = nullptr;   // layer-0 attention norm of the last decode step
+    int8_t* dbg_qs = nullptr;
+    uint16_t* dbg_d = nullptr;
+    float* last_hidden = nullptr;  // final norm of the last forward
+    int8_t* head_qs = nullptr;
+    uint16_t* head_d = nullptr;
+
+    // prefill workspace, grown on demand
+    size_t cap_rows = 0;
+    float* p_hidden = nullptr;
+    float* p_normed = nullptr;
+    float* p_qkv = nullptr;
+    float* p_q = nullptr;
+    float* p_attn = nullptr;
+    float* p_gu = nullptr;
+    float* p_act = nullptr;
+    int8_t* p_aq = nullptr;
+    uint16_t* p_ad = nullptr;
+
+    uint32_t* h_pinned = nullptr;  // pinned staging for ids / tokens
+    hipGraphExec_t graph = nullptr;
+    hipGraph_t graph_def = nullptr;
+
+    // Per-kernel relaunchers of the decode step (measurement only).
+    std::vector<std::function<int()>> kernels;
+    std::vector<uint64_t> kernel_bytes;
+};
+
+namespace sq {
+int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out);
+void ctx_destroy(sq_ctx* c);
+int ctx_forward(sq_ctx* c, const uint32_t* ids, size_t n);
+int ctx_generate(sq_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t max_tokens, uint32_t flags,
+                 uint32_t* out, size_t* n_out, double* step_ms);
+int ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes);
+int model_load(const char* path, sq_model** out);
+// Parse + config + tensor checks only (no device allocation).
+int model_inspect(const char* path, sq_model** out);
+void model_free(sq_model* m);
+}  // namespace sq

@@ -1,0 +1,256 @@
+"""Model-level parity on the GPU: full forward passes vs the oracle.
+
+The oracle runs the same GGUF file in the matching arithmetic mode (W8A8
+integer path for Q8_0 / Q4_0, f32 activations for BF16 and the
+SQUIRREL_F32_ACTS ablation).  Logits are compared teacher-forced: both sides
+consume the same token ids at every step, so one rounding difference cannot
+snowball into a different continuation.
+
+Tolerance rule (integer path).  Activation quantization makes W8A8 logits
+discontinuous in f32 rounding: a 1-ulp difference before a Q8 rounding step
+moves that activation by a whole quantum.  The reference's own two builds (the
+aarch64 NEON combine order vs its scalar twin) therefore either agree to
+~1e-7 relative or differ by 0.7-1.0x the whole W8A8-vs-W8A32 quantization
+error (measured on these models, 8 seeds).  The bar for the GPU is the same:
+per step, the relative L2 error of the GPU logits against the oracle's W8A8
+logits must not exceed the reference's own W8A8-vs-W8A32 relative L2 error on
+the same inputs (REL_TOL_FACTOR x that gap).  Integer parity itself is pinned
+bit for bit at the kernel level (quantizer, block sums, fused norm+quantize).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+sq = pytest.importorskip("sqhip")
+
+REL_TOL_FACTOR = 1.0
+LOGIT_ABS_FLOOR = 2e-4
+MODES = {"Q8_0": O.W8A8, "Q4_0": O.W8A8, "BF16": O.W8A32}
+A32_SKIP = ("f32-activation kernels (BF16, SQUIRREL_F32_ACTS) are switched off after a GPU "
+            "memory fault in a BF16 model prefill whose cause is not identified yet")
+
+
+def run_oracle(path, seq, mode, max_pos=256):
+    m = O.OracleModel(path)
+    c = m.new_context(max_pos, mode)
+    outs = []
+    c.forward(seq[0])
+    outs.append(c.logits())
+    for t in seq[1:]:
+        c.forward([t])
+        outs.append(c.logits())
+    return outs
+
+
+def run_gpu(path, seq, f32_acts=False, graph=True, max_pos=256):
+    m = sq.Llama3_2(path)
+    c = m.new_context(max_pos, f32_acts=f32_acts, graph=graph)
+    outs, toks = [], []
+    c.forward(seq[0])
+    outs.append(c.logits())
+    toks.append(c.argmax())
+    for t in seq[1:]:
+        c.forward([t])
+        outs.append(c.logits())
+        toks.append(c.argmax())
+    return outs, toks, (m, c)
+
+
+def teacher_seq(vocab, n_prompt=13, n_decode=6, seed=0):
+    r = np.random.default_rng(seed)
+    prompt = r.integers(0, vocab, n_prompt).astype(np.uint32)
+    return [prompt] + [int(t) for t in r.integers(0, vocab, n_decode)]
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / np.linalg.norm(b))
+
+
+def check_logits(path, seq, got, label):
+    want = run_oracle(path, seq, O.W8A8)
+    f32 = run_oracle(path, seq, O.W8A32)
+    neon = run_oracle(path, seq, O.W8A8_NEON)
+    rows = []
+    for step, (g, w, f, n) in enumerate(zip(got, want, f32, neon)):
+        e_gpu, e_q, e_ref = rel_l2(g, w), rel_l2(w, f), rel_l2(n, w)
+        rows.append((step, e_gpu, e_q, e_ref, float(np.abs(g - w).max())))
+    print(f"{label}: step, rel_l2(gpu, oracle W8A8), rel_l2(W8A8, W8A32), rel_l2(neon, scalar), max|d|")
+    for r in rows:
+        print("   %2d  %.2e  %.2e  %.2e  %.2e" % r)
+    for step, e_gpu, e_q, e_ref, mx in rows:
+        assert e_gpu <= REL_TOL_FACTOR * e_q, f"step {step}: {e_gpu:.3e} > {REL_TOL_FACTOR} x {e_q:.3e}"
+    return rows
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0", "BF16"])
+@pytest.mark.parametrize("variant", ["g4", "g2"])
+def test_teacher_forced_logits(tiny_gguf, wtype, variant):
+    if wtype == "BF16":
+        pytest.skip(A32_SKIP)
+    path = tiny_gguf(wtype, variant)
+    cfg = O.OracleModel(path).cfg
+    seq = teacher_seq(cfg.vocab)
+    got, toks, _ = run_gpu(path, seq)
+    check_logits(path, seq, got, f"{wtype}/{variant}")
+    for g, t in zip(got, toks):
+        assert t == O.greedy(g), "device argmax disagrees with the greedy rule on its own logits"
+
+
+def test_f32_acts_ablation(tiny_gguf):
+    """SQUIRREL_F32_ACTS=1 (linear.rs:14-19): W8A32 on both sides."""
+    path = tiny_gguf("Q8_0", "g4")
+    seq = teacher_seq(2048, seed=3)
+    want = run_oracle(path, seq, O.W8A32)
+    got, _, _ = run_gpu(path, seq, f32_acts=True)
+    err = max(float(np.abs(g - w).max()) for g, w in zip(got, want))
+    print(f"W8A32 max|dlogit| {err:.2e}")
+    assert err <= LOGIT_ABS_FLOOR * 5
+
+
+def test_fused_norm_quantize_bit_exact(tiny_gguf):
+    """The decode step's fused RMSNorm+quantize prologue: its Q8_0 blocks are
+    bit-identical to the reference quantizer applied to its f32 output, and
+    that f32 output matches the oracle's RMSNorm within rounding."""
+    path = tiny_gguf("Q8_0", "g4")
+    m = sq.Llama3_2(path)
+    c = m.new_context(64)
+    c.forward(np.array([5, 6, 7], np.uint32))
+    c.forward([11])
+    normed, blocks = c.debug_act()
+    want = O.quantize_row_q8_0(normed)
+    assert np.array_equal(blocks["d"], want["d"]) and np.array_equal(blocks["qs"], want["qs"])
+    om = O.OracleModel(path)
+    x = O.embed([11], om.wtype, om.g.tensor_bytes("token_embd.weight"), om.cfg.embed_dim, om.cfg.vocab)
+    w = np.frombuffer(om.g.tensor_bytes("blk.0.attn_norm.weight").tobytes(), np.float32)
+    ref = O.rms_norm(x, w, om.cfg.rms_eps)[0]
+    assert np.allclose(normed, ref, rtol=2e-6, atol=1e-7)
+
+
+def test_graph_matches_eager(tiny_gguf):
+    path = tiny_gguf("Q8_0", "g4")
+    seq = teacher_seq(2048, seed=5)
+    a, ta, _ = run_gpu(path, seq, graph=True)
+    b, tb, _ = run_gpu(path, seq, graph=False)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    assert ta == tb
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "BF16"])
+def test_generate_matches_forward_loop(tiny_gguf, wtype):
+    """TextTokenGenerator::generate == forward/sample loop, and the greedy
+    sequence vs the oracle's (first divergence reported, not asserted beyond
+    the steps whose top-2 margin exceeds the logit tolerance)."""
+    if wtype == "BF16":
+        pytest.skip(A32_SKIP)
+    path = tiny_gguf(wtype, "g4")
+    m = sq.Llama3_2(path)
+    c = m.new_context(128)
+    prompt = np.random.default_rng(1).integers(0, 2048, 9).astype(np.uint32)
+    gen, ms = sq.TextTokenGenerator(m, c).generate(prompt, 20, ignore_eos=True)
+    assert len(gen) == 20 and np.all(ms > 0)
+    c2 = m.new_context(128)
+    c2.forward(prompt)
+    loop = [c2.argmax()]
+    for _ in range(19):
+        c2.forward([loop[-1]])
+        loop.append(c2.argmax())
+    assert gen == loop
+    om = O.OracleModel(path)
+    oc = om.new_context(128, MODES[wtype])
+    oc.forward(prompt)
+    ref = []
+    for step in range(20):
+        lg = oc.logits()
+        ref.append(O.greedy(lg))
+        srt = np.sort(lg)
+        if ref[-1] != gen[step]:
+            margin = float(srt[-1] - srt[-2])
+            print(f"greedy diverges at step {step} (oracle top-2 margin {margin:.2e})")
+            assert margin <= 0.1
+            break
+        oc.forward([ref[-1]])
+
+
+def test_eos_stops_generation(tiny_gguf, model_dir):
+    """EOS handling (text_generator.rs:68-74): the same weights with EOS set to
+    a token the model emits stop the loop just before it; IGNORE_EOS runs on."""
+    from conftest import TINY
+    path = tiny_gguf("Q8_0", "g4")
+    prompt = np.array([1, 2, 3, 4], np.uint32)
+    m = sq.Llama3_2(path)
+    full, _ = sq.TextTokenGenerator(m, m.new_context(64)).generate(prompt, 12, ignore_eos=True)
+    eos = full[3]
+    cut = full.index(eos)
+    path2 = str(model_dir / "tiny_eos.gguf")
+    sq.write_synthetic_gguf(path2, "Q8_0", seed=7, eos=eos, **TINY)
+    m2 = sq.Llama3_2(path2)
+    stopped, _ = sq.TextTokenGenerator(m2, m2.new_context(64)).generate(prompt, 12)
+    assert stopped == full[:cut]
+    ran, _ = sq.TextTokenGenerator(m2, m2.new_context(64)).generate(prompt, 12, ignore_eos=True)
+    assert ran == full
+
+
+def test_no_kv_cache_mode(tiny_gguf):
+    """SQUIRREL_NO_KV_CACHE=1 (text_generator.rs:76-78) recomputes the whole
+    sequence every step and yields the same tokens as the cached loop."""
+    path = tiny_gguf("Q8_0", "g4")
+    m = sq.Llama3_2(path)
+    prompt = np.random.default_rng(2).integers(0, 2048, 6).astype(np.uint32)
+    a, _ = sq.TextTokenGenerator(m, m.new_context(64)).generate(prompt, 6, ignore_eos=True)
+    b, _ = sq.TextTokenGenerator(m, m.new_context(64)).generate(prompt, 6, ignore_eos=True,
+                                                                 no_kv_cache=True)
+    # Prefill and decode use different kernels, so a near-tie can flip; the
+    # first token (identical computation) must agree.
+    assert a[0] == b[0]
+
+
+def test_a32_paths_refuse_loudly(tiny_gguf):
+    """The switched-off paths fail with an error instead of running."""
+    with pytest.raises(sq.LLMError) as e:
+        sq.Llama3_2(tiny_gguf("BF16", "g4"))
+    assert e.value.code == 20
+    m = sq.Llama3_2(tiny_gguf("Q8_0", "g4"))
+    with pytest.raises(sq.LLMError):
+        m.new_context(16, f32_acts=True)
+
+
+def test_errors(tiny_gguf):
+    path = tiny_gguf("Q8_0", "g4")
+    m = sq.Llama3_2(path)
+    c = m.new_context(8)
+    with pytest.raises(sq.KernelError) as e:
+        c.forward(np.array([], np.uint32))
+    assert e.value.kind == "EmptyInput"
+    with pytest.raises(sq.LLMError):
+        c.forward(np.arange(9, dtype=np.uint32))  # more positions than the cache holds
+    c.forward(np.arange(8, dtype=np.uint32))
+    with pytest.raises(sq.LLMError):
+        c.forward([1])
+
+
+@pytest.mark.skipif(os.environ.get("SQHIP_SKIP_FULL") == "1", reason="full-size model skipped")
+def test_full_size_q8_0_prefill_and_decode(model_dir):
+    """Llama-3.2-1B shape, Q8_0: 32-token prefill then 3 decode steps,
+    teacher-forced against the oracle's W8A8 path."""
+    path = str(model_dir / "llama1b_q8_0.gguf")
+    if not os.path.exists(path):
+        sq.write_synthetic_gguf(path, "Q8_0", seed=0)
+    r = np.random.default_rng(0)
+    seq = [r.integers(0, 128256, 32).astype(np.uint32)] + [int(t) for t in r.integers(0, 128256, 3)]
+    O.set_threads(min(16, os.cpu_count() or 1))
+    got, toks, _ = run_gpu(path, seq, max_pos=64)
+    want = run_oracle(path, seq, O.W8A8, max_pos=64)
+    f32 = run_oracle(path, seq, O.W8A32, max_pos=64)
+    for step, (g, w, f) in enumerate(zip(got, want, f32)):
+        e_gpu, e_q = rel_l2(g, w), rel_l2(w, f)
+        print(f"full-size Q8_0 step {step}: rel_l2 gpu/oracle {e_gpu:.2e}, W8A8/W8A32 {e_q:.2e}, "
+              f"max|d| {float(np.abs(g - w).max()):.2e}, top1 gpu {int(np.argmax(g))} oracle {int(np.argmax(w))}")
+        assert e_gpu <= REL_TOL_FACTOR * e_q
+    for g, t in zip(got, toks):
+        assert t == O.greedy(g)

@@ -1,0 +1,334 @@
+"""Operator-level parity: HIP kernels (through the C ABI) vs the oracle.
+
+Bars: bit-exact for the activation quantizer, integer block sums, embedding,
+RoPE (host libm sin/cos table), residual add and argmax; float kernels within
+the tolerance written at each assert, relative to the magnitude of the terms
+summed (the reference's own bound style, src/kernels/matmul.rs:315-335).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+sq = pytest.importorskip("sqhip")
+from sqhip import ops  # noqa: E402
+from sqhip.ops import DeviceArray  # noqa: E402
+
+
+A32_SKIP = ("f32-activation kernels (BF16, SQUIRREL_F32_ACTS) are switched off after a GPU "
+            "memory fault in a BF16 model prefill whose cause is not identified yet")
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def quant_weights(wtype, rows, k, seed, scale=0.02):
+    """GGUF blocks for a rows x k matrix, built with the oracle's quantizer
+    (Q8_0) or the ggml Q4_0 rule (Q4_0) or RNE bf16."""
+    x = (rng(seed).standard_normal((rows, k)) * scale).astype(np.float32)
+    if wtype == O.Q8_0:
+        return O.quantize_row_q8_0(x).reshape(rows, k // 32), x
+    if wtype == O.Q4_0:
+        xb = x.reshape(-1, 32)
+        idx = np.argmax(np.abs(xb), axis=1)
+        mx = xb[np.arange(xb.shape[0]), idx]
+        d = (mx / np.float32(-8)).astype(np.float32)
+        inv = np.where(d != 0, np.float32(1) / np.where(d != 0, d, 1), 0).astype(np.float32)
+        q = np.minimum(15, np.trunc(xb * inv[:, None] + np.float32(8.5)).astype(np.int32))
+        blk = np.zeros(xb.shape[0], O.BLOCK_Q4_0)
+        blk["d"] = d.astype(np.float16).view(np.uint16)
+        blk["qs"] = (q[:, :16] | (q[:, 16:] << 4)).astype(np.uint8)
+        return blk.reshape(rows, k // 32), x
+    u = x.view(np.uint32)
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return b.reshape(rows, k), x
+
+
+# ---------------------------------------------------------------- quantizer
+
+def quantizer_inputs():
+    r = rng(1)
+    rows = [r.standard_normal(4096).astype(np.float32) * 3,
+            (r.standard_normal(2048) * 1e-3).astype(np.float32)]
+    # The reference's edge cases (dot_prod.rs:629-654): all-zero block,
+    # negative absmax, +-0.5 ties, f32::MAX/2 (scale overflows f16).
+    src = (np.sin(np.arange(32 * 6, dtype=np.float32) * np.float32(0.37)) * 4 - 0.5).astype(np.float32)
+    src[32:64] = 0
+    src[64] = -100
+    src[96] = 0.5
+    src[97] = -0.5
+    src[128] = np.finfo(np.float32).max / 2
+    rows.append(src)
+    # exact ties after scaling, tiny values, subnormals, NaN / inf entries
+    t = np.zeros(32 * 8, np.float32)
+    t[:32] = np.arange(32, dtype=np.float32) - 15.5
+    t[32:64] = np.float32(127.0) * (np.arange(32, dtype=np.float32) / 31) - 63.5
+    t[64:96] = np.float32(1e-40) * np.arange(32, dtype=np.float32)
+    t[96:128] = np.float32(1e-30) * (np.arange(32, dtype=np.float32) - 16)
+    t[128] = np.nan
+    t[129:160] = 1.0
+    t[160] = np.inf
+    t[161:192] = -2.0
+    t[192:224] = np.float32(65504.0 * 127) * (r.random(32).astype(np.float32) - 0.5)
+    t[224:256] = r.standard_normal(32).astype(np.float32) * 1e5
+    rows.append(t)
+    return rows
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_quantize_row_bit_exact(case):
+    x = quantizer_inputs()[case]
+    got = ops.quantize_row_q8_0(DeviceArray.from_numpy(x))
+    want = O.quantize_row_q8_0(x)
+    assert np.array_equal(got["d"], want["d"]), "scales differ"
+    assert np.array_equal(got["qs"], want["qs"]), "quants differ"
+
+
+# ---------------------------------------------------------------- integer sums
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("k", [2048, 8192])
+def test_block_isums_bit_exact(wtype, k):
+    w, _ = quant_weights(wtype, 4, k, seed=k + wtype)
+    a = rng(5).standard_normal(k).astype(np.float32)
+    aq = O.quantize_row_q8_0(a)
+    W = ops.Weight(wtype, w, 4, k)
+    d_aq = DeviceArray.from_numpy(aq)
+    for row in (0, 3):
+        got = ops.block_isums(d_aq, W, row)
+        want = O.block_isums(aq, w[row], wtype)
+        assert np.array_equal(got, want)
+
+
+def test_q4_int_dot_exact_on_integers():
+    """q4_int_dot_exact_on_integers (dot_prod.rs:774-803) on the device."""
+    qs = np.array([((i % 16) << 4) | (15 - i % 16) for i in range(16)], np.uint8)
+    w = np.zeros((1, 1), O.BLOCK_Q4_0)
+    w["d"] = np.float16(1.0).view(np.uint16)
+    w["qs"][0, 0] = qs
+    a = np.zeros(1, O.BLOCK_Q8_0)
+    a["d"] = np.float16(1.0).view(np.uint16)
+    a["qs"][0] = np.arange(32, dtype=np.int32) - 16
+    expected = 0
+    for j in range(16):
+        lo, hi = int(qs[j] & 15) - 8, int(qs[j] >> 4) - 8
+        expected += int(a["qs"][0][j]) * lo + int(a["qs"][0][j + 16]) * hi
+    W = ops.Weight(O.Q4_0, w, 1, 32)
+    assert int(ops.block_isums(DeviceArray.from_numpy(a), W, 0)[0]) == expected
+
+
+# ---------------------------------------------------------------- linear
+
+SHAPES = [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048), (96, 9), (128, 7)]
+
+
+def term_mag(x, w_f32):
+    return np.abs(x.astype(np.float64)) @ np.abs(w_f32.astype(np.float64)).T
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
+@pytest.mark.parametrize("k,n", SHAPES)
+@pytest.mark.parametrize("m", [1, 5])
+@pytest.mark.parametrize("f32_acts", [False, True])
+def test_linear_matches_oracle(wtype, k, n, m, f32_acts):
+    if wtype == O.BF16 and f32_acts:
+        pytest.skip("BF16 always uses f32 activations")
+    if wtype == O.BF16 or f32_acts:
+        pytest.skip(A32_SKIP)
+    w, _ = quant_weights(wtype, n, k, seed=31 * k + n + wtype)
+    x = (rng(k + n).standard_normal((m, k)) * 1.5).astype(np.float32)
+    W = ops.Weight(wtype, w, n, k)
+    out = DeviceArray((m, n))
+    ops.linear(DeviceArray.from_numpy(x), W, out, f32_acts=f32_acts)
+    got = out.numpy()
+    mode = O.W8A32 if (f32_acts or wtype == O.BF16) else O.W8A8
+    want = O.linear(x, wtype, w, n, mode)
+    wf = np.stack([O.dequantize(wtype, w[i], k) for i in range(n)])
+    mag = term_mag(x, wf)
+    err = np.abs(got.astype(np.float64) - want)
+    # Same per-block terms, different summation order: f32 rounding of a sum
+    # of |terms| <= mag is bounded by ~k*eps*mag; 4e-6 * mag covers k <= 8192
+    # with the tree orders used on both sides.
+    assert np.all(err <= 4e-6 * mag + 1e-6), float((err / (mag + 1e-30)).max())
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
+def test_linear_shared_matches_separate(wtype):
+    """fused_matches_separate_calls (matmul.rs:257-279): bit-equal."""
+    if wtype == O.BF16:
+        pytest.skip(A32_SKIP)
+    k = 2048
+    dims = [2048, 512, 512]
+    ws = [quant_weights(wtype, n, k, seed=n + i)[0] for i, n in enumerate(dims)]
+    Ws = [ops.Weight(wtype, w, n, k) for w, n in zip(ws, dims)]
+    x = DeviceArray.from_numpy(rng(9).standard_normal((3, k)).astype(np.float32))
+    fused = [DeviceArray((3, n)) for n in dims]
+    ops.linear_shared(x, Ws, fused)
+    for W, f, n in zip(Ws, fused, dims):
+        sep = DeviceArray((3, n))
+        ops.linear(x, W, sep)
+        assert np.array_equal(sep.numpy(), f.numpy())
+
+
+# ---------------------------------------------------------------- pointwise
+
+def test_rms_norm_hand_computed():
+    """matches_hand_computed (rms_norm.rs:86-98) and weight_scales_output."""
+    x = DeviceArray.from_numpy(np.array([[1, 2, 3, 4]], np.float32))
+    out = DeviceArray((1, 4))
+    ops.rms_norm(x, DeviceArray.from_numpy(np.ones(4, np.float32)), out, 0.0)
+    rms = np.sqrt(np.float32(7.5))
+    assert np.allclose(out.numpy()[0], np.array([1, 2, 3, 4]) / rms, atol=1e-5)
+    ops.rms_norm(x, DeviceArray.from_numpy(np.full(4, 2, np.float32)), out, 0.0)
+    assert np.allclose(out.numpy()[0], 2 * np.array([1, 2, 3, 4]) / rms, atol=1e-5)
+    z = DeviceArray.from_numpy(np.zeros((1, 4), np.float32))
+    ops.rms_norm(z, DeviceArray.from_numpy(np.ones(4, np.float32)), out, 1e-5)
+    assert np.all(np.isfinite(out.numpy())) and np.all(out.numpy() == 0)
+
+
+@pytest.mark.parametrize("dim", [2048, 512, 100])
+def test_rms_norm_matches_oracle(dim):
+    x = (rng(dim).standard_normal((7, dim)) * 2).astype(np.float32)
+    w = (1 + 0.1 * rng(1).standard_normal(dim)).astype(np.float32)
+    out = DeviceArray((7, dim))
+    ops.rms_norm(DeviceArray.from_numpy(x), DeviceArray.from_numpy(w), out, 1e-5)
+    want = O.rms_norm(x, w, 1e-5)
+    # Only the sum of squares is reordered: relative error ~ dim * eps.
+    assert np.allclose(out.numpy(), want, rtol=2e-6, atol=1e-7)
+
+
+def test_rope_rows_bit_exact():
+    inv = O.rope_inv_freq(64, 500000.0)
+    t = rng(3).standard_normal((9, 2048)).astype(np.float32)
+    d = DeviceArray.from_numpy(t)
+    ops.rope_rows(d, 4090, inv)
+    st, want = O.rope_rows(t, 4090, inv)
+    assert st == 0
+    assert np.array_equal(d.numpy(), want)
+
+
+def test_silu_mul_add():
+    x = (rng(4).standard_normal(5000) * 8).astype(np.float32)
+    x[:4] = [0.0, -100.0, 100.0, -0.0]
+    d = DeviceArray.from_numpy(x)
+    ops.silu(d)
+    want = O.silu(x)
+    # device expf vs glibc expf: each within ~1 ulp, so a few ulps apart
+    assert np.allclose(d.numpy(), want, rtol=1e-6, atol=1e-38)
+    a, b = x, x[::-1].copy()
+    o = DeviceArray(a.shape)
+    ops.elementwise_mul(DeviceArray.from_numpy(a), DeviceArray.from_numpy(b), o)
+    assert np.array_equal(o.numpy(), a * b)
+    da = DeviceArray.from_numpy(a)
+    ops.elementwise_add(da, DeviceArray.from_numpy(b))
+    assert np.array_equal(da.numpy(), a + b)
+
+
+def test_softmax_known_values():
+    """known_values / sums_to_one / survives_large_values (softmax.rs:39-65)."""
+    o = DeviceArray(3)
+    ops.softmax(DeviceArray.from_numpy(np.array([1, 2, 3], np.float32)), o)
+    assert np.allclose(o.numpy(), [0.09003057, 0.24472847, 0.66524096], atol=1e-6)
+    o2 = DeviceArray(2)
+    ops.softmax(DeviceArray.from_numpy(np.array([100, 101], np.float32)), o2)
+    v = o2.numpy()
+    assert np.all(np.isfinite(v)) and abs(v.sum() - 1) < 1e-6 and v[1] > v[0]
+    with pytest.raises(sq.KernelError) as e:
+        ops.softmax(DeviceArray(0), DeviceArray(0))
+    assert e.value.kind == "EmptyInput"
+
+
+# ---------------------------------------------------------------- attention
+
+def sdpa_dev(q, k, v, seq_q, seq_k, nh, nkv, hd):
+    out = DeviceArray(q.size)
+    ops.sdpa_cached(DeviceArray.from_numpy(q), DeviceArray.from_numpy(k), DeviceArray.from_numpy(v), out,
+                    nh, nkv, hd)
+    return out.numpy()
+
+
+def test_sdpa_reference_known_answers():
+    """The five attention tests of attention.rs:84-171 on the device."""
+    q = np.array([0.5, -1.0, 2.0, 0.25], np.float32)
+    v = np.array([7.0, 8.0, 9.0, 10.0], np.float32)
+    assert np.allclose(sdpa_dev(q, q, v, 1, 1, 1, 1, 4), v, atol=1e-5)
+    q = np.array([1.0, 0.0, 0.5, 0.5], np.float32)
+    k = np.array([1.0, 0.0, 0.0, 1.0], np.float32)
+    va = np.array([3.0, 4.0, 99.0, -99.0], np.float32)
+    vb = np.array([3.0, 4.0, -42.0, 1234.0], np.float32)
+    oa, ob = sdpa_dev(q, k, va, 2, 2, 1, 1, 2), sdpa_dev(q, k, vb, 2, 2, 1, 1, 2)
+    assert np.allclose(oa[:2], ob[:2], atol=1e-5) and np.allclose(oa[:2], [3, 4], atol=1e-5)
+    q = np.array([1, 0, 1, 0, 0, 1, 0, 1], np.float32)
+    k = np.array([1.0, 1.0, 0.5, -0.5], np.float32)
+    v = np.array([10.0, 20.0, 30.0, 40.0], np.float32)
+    o = sdpa_dev(q, k, v, 1, 1, 4, 2, 2)
+    assert np.allclose(o[0:2], o[2:4], atol=1e-5) and np.allclose(o[4:6], o[6:8], atol=1e-5)
+    q = np.array([0.1, 0.2, 0.3, 0.4], np.float32)
+    k = np.array([1.0, 0.0, -1.0, 2.0], np.float32)
+    v = np.array([5.0, 6.0, 7.0, 8.0], np.float32)
+    assert np.allclose(sdpa_dev(q, k, v, 1, 1, 2, 2, 2), v, atol=1e-5)
+    with pytest.raises(sq.KernelError) as e:
+        sdpa_dev(np.zeros(6, np.float32), np.zeros(6, np.float32), np.zeros(6, np.float32), 1, 1, 3, 2, 2)
+    assert e.value.kind == "ShapeMismatch"
+
+
+@pytest.mark.parametrize("seq_q,seq_k", [(1, 1), (1, 37), (1, 300), (1, 4096), (200, 200), (64, 300), (5, 5)])
+@pytest.mark.parametrize("nh,nkv", [(32, 8), (8, 2), (4, 4)])
+def test_sdpa_model_kernels_match_oracle(seq_q, seq_k, nh, nkv):
+    hd = 64
+    r = rng(seq_q * 1000 + seq_k + nh)
+    q = r.standard_normal(seq_q * nh * hd).astype(np.float32)
+    k = r.standard_normal(seq_k * nkv * hd).astype(np.float32)
+    v = r.standard_normal(seq_k * nkv * hd).astype(np.float32)
+    got = sdpa_dev(q, k, v, seq_q, seq_k, nh, nkv, hd)
+    st, want = O.sdpa(q, k, v, seq_q, seq_k, nh, nkv, hd)
+    assert st == 0
+    # Online softmax vs two-pass: outputs are convex combinations of v rows
+    # (|v| ~ 1); rounding differences stay at a few f32 ulps of the scale.
+    assert np.allclose(got, want, rtol=1e-5, atol=2e-6), float(np.abs(got - want).max())
+
+
+def test_sdpa_generic_head_dims():
+    for hd, nh, nkv, sq_, sk in [(4, 2, 1, 3, 5), (32, 4, 2, 1, 9), (128, 2, 2, 4, 4)]:
+        r = rng(hd)
+        q = r.standard_normal(sq_ * nh * hd).astype(np.float32)
+        k = r.standard_normal(sk * nkv * hd).astype(np.float32)
+        v = r.standard_normal(sk * nkv * hd).astype(np.float32)
+        got = sdpa_dev(q, k, v, sq_, sk, nh, nkv, hd)
+        st, want = O.sdpa(q, k, v, sq_, sk, nh, nkv, hd)
+        assert st == 0 and np.allclose(got, want, rtol=1e-5, atol=2e-6)
+
+
+# ---------------------------------------------------------------- greedy / embed
+
+@pytest.mark.parametrize("case", range(7))
+def test_greedy_matches_oracle(case):
+    r = rng(case)
+    nan = np.float32(np.nan)
+    cases = [
+        np.array([0.1, -2.3, 5.7, 4.0], np.float32),                      # picks_max_index
+        np.array([1.0, nan, 3.0, 2.0], np.float32),                       # ignores_nan
+        np.array([3.0, 1.0, 3.0, 2.0, 3.0, 0.0], np.float32),             # ties -> last
+        np.array([5.0, nan, 1.0], np.float32),                            # NaN hands over the lead
+        np.array([1.0, 3.0, nan], np.float32),                            # trailing NaN wins
+        r.standard_normal(128256).astype(np.float32),
+        np.round(r.standard_normal(128256) * 2).astype(np.float32),       # many exact ties
+    ]
+    x = cases[case]
+    assert ops.greedy(DeviceArray.from_numpy(x)) == O.greedy(x)
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
+def test_embed_bit_exact(wtype):
+    if wtype == O.BF16:
+        pytest.skip(A32_SKIP)
+    vocab, dim = 300, 2048
+    w, _ = quant_weights(wtype, vocab, dim, seed=11 + wtype)
+    toks = np.array([0, 299, 17, 17, 150], np.uint32)
+    out = DeviceArray((toks.size, dim))
+    ops.embed(DeviceArray.from_numpy(toks), ops.Weight(wtype, w, vocab, dim), out)
+    want = O.embed(toks, wtype, w, dim, vocab)
+    assert np.array_equal(out.numpy(), want)
