@@ -96,6 +96,32 @@ def cpu_baseline(path: str, prompt: np.ndarray, n_decode: int) -> dict:
                       f"(f32 activations, W8A32), {threads} threads"}
 
 
+def copy_calibration(mib: int) -> int:
+    """A plain HBM-to-HBM copy of known size, for scaling PMC byte counters."""
+    import torch
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 5 copies of {n} bytes (read {n}, write {n} per copy)")
+    return 0
+
+
+def measured_traffic(config: str):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by the copy calibration),
+    or None when no measurement exists for this workload."""
+    path = os.path.join(REPO, "profiles", f"traffic_gate_up_matvec_{config}.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,13 +130,20 @@ def main() -> int:
     ap.add_argument("--config", default="q8", choices=sorted(CONFIGS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=12)
+    ap.add_argument("--cpu-steps", type=int, default=None,
+                    help="decode steps timed on the CPU (default: the same count as the GPU run)")
     ap.add_argument("--kernel-iters", type=int, default=200)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB five times (the known-size "
+                         "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the token loop is a "
               "batch-1 single-device workload); run with --gpus 1", file=sys.stderr)
         return 2
+
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
 
     import sqhip
     cfg = CONFIGS[args.config]
@@ -151,14 +184,14 @@ def main() -> int:
                          "gbs": round(nbytes / us / 1e3, 1)}
     dom = kernels["gate_up_matvec"]
     roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
                 "kernel": "gate_up_matvec (layer 0: RMSNorm+Q8 prologue, 16384x2048 Q8_0 "
                           "matvec, SiLU*up+Q8 epilogue)"}
 
     cpu = None
     if not args.no_cpu:
         t1 = time.time()
-        cpu = cpu_baseline(path, prompt[:32], args.cpu_steps)
+        cpu = cpu_baseline(path, prompt[:32], args.cpu_steps if args.cpu_steps is not None else min(K, 64))
         log(f"cpu baseline {cpu['value']} tok/s in {time.time() - t1:.1f}s")
 
     line = {

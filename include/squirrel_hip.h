@@ -158,8 +158,10 @@ void sq_weight_free(sq_weight* w);
  * GGUF layout. */
 int sq_quantize_row_q8_0(const float* d_x, size_t n, void* d_blocks);
 /* linear (src/ops/linear.rs:26-70): d_out[m, rows] = d_in[m, k] @ W.  Q8_0 /
- * Q4_0 quantize the activations (the reference's aarch64 path) unless
- * SQ_CTX_F32_ACTS is set in flags; BF16 always keeps f32 activations. */
+ * Q4_0 quantize the activations (the reference's aarch64 path).  The
+ * f32-activation kernels (SQ_CTX_F32_ACTS in flags, and BF16 weights, which
+ * always take f32 activations) are disabled in this build and return
+ * SQ_ERR_UNSUPPORTED. */
 int sq_linear(const float* d_in, size_t m, size_t k, const sq_weight* w, float* d_out,
               uint32_t flags);
 /* linear_shared (src/ops/linear.rs:73-168): several projections of one input,
@@ -194,10 +196,12 @@ int sq_softmax(const float* d_in, float* d_out, size_t n);
 /* ---- measurement -----------------------------------------------------
  * Replays one kernel of the context's decode step `iters` times on the
  * context stream between two HIP events and returns the mean duration.
- * which: 0 = fused gate/up matvec of layer 0, 1 = LM head, 2 = down matvec,
- * 3 = QKV matvec, 4 = attention, 5 = o-projection.  The context must have run
- * at least one decode step; the replays write the same buffers the step does,
- * so reset or re-prefill the context afterwards. */
+ * which: 0 = fused gate/up matvec, 1 = LM head (+ argmax), 2 = down matvec,
+ * 3 = QKV matvec, 4 = attention, 5 = o-projection; the per-layer kernels are
+ * those of layer 1 (layer 0 when the model has one layer).  The context must
+ * have run at least one decode step and have a free KV position (replays
+ * write the KV row at the current position); the replays write the same
+ * buffers the step does, so reset or re-prefill the context afterwards. */
 int sq_ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes);
 
 #ifdef __cplusplus

@@ -371,19 +371,18 @@ int sq_sdpa(const float* d_q, const float* d_k, const float* d_v, float* d_out, 
     const bool model_kernels = head_dim == 64 && (G == 1 || G == 2 || G == 4 || G == 8);
     int st;
     if (model_kernels && seq_q == 1) {
-        // The decode kernels: the query sits at position seq_k - 1.
-        const int nsplit = (int)std::min<size_t>(64, std::max<size_t>(1, ((seq_k + 63) / 64 + 1) / 2));
-        Tmp pos, pm, pl, po;
+        // The decode kernel: the query sits at position seq_k - 1.
+        const int tiles = (int)((seq_k + 63) / 64);
+        Tmp pos, pm, pl, po, cnt, aq, ad;
         const int p = (int)seq_k - 1;
-        if ((st = pos.alloc(4)) || (st = pm.alloc(n_heads * nsplit * 4)) || (st = pl.alloc(n_heads * nsplit * 4)) ||
-            (st = po.alloc(n_heads * nsplit * 64 * 4)))
+        if ((st = pos.alloc(4)) || (st = pm.alloc(n_heads * tiles * 4)) || (st = pl.alloc(n_heads * tiles * 4)) ||
+            (st = po.alloc(n_heads * tiles * 64 * 4)) || (st = cnt.alloc(n_kv_heads * 4)))
             return st;
         SQ_HIP_CHECK(hipMemcpy(pos.p, &p, 4, hipMemcpyHostToDevice));
-        if ((st = launch_attn_decode(nullptr, d_q, d_k, d_v, (const int*)pos.p, (int)n_heads, (int)n_kv_heads, 64,
-                                     nsplit, (float*)pm.p, (float*)pl.p, (float*)po.p)))
-            return st;
-        return finish(launch_attn_combine(nullptr, (float*)pm.p, (float*)pl.p, (float*)po.p, (int)n_heads, 64, nsplit,
-                                          d_out, nullptr, nullptr));
+        SQ_HIP_CHECK(hipMemset(cnt.p, 0, n_kv_heads * 4));
+        return finish(launch_attn_decode(nullptr, d_q, d_k, d_v, (const int*)pos.p, (int)n_heads, (int)n_kv_heads, 64,
+                                         tiles, (float*)pm.p, (float*)pl.p, (float*)po.p, (unsigned*)cnt.p, d_out,
+                                         nullptr, nullptr));
     }
     if (model_kernels) {
         return finish(launch_attn_prefill(nullptr, d_q, d_k, d_v, (int)(seq_k - seq_q), (int)seq_q, (int)n_heads,

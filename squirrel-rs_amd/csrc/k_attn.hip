@@ -21,123 +21,123 @@ inline int check_launch(const char* what) {
     return 0;
 }
 
-// Decode attention, flash-decoding split over positions.  One wavefront per
-// (kv head, split); it owns the GQA group's G query heads, so each K/V row is
-// read once for all of them.  Tile = 64 positions: lane = position for the
-// scores, lane = dimension for P*V.
+// Decode attention.  One workgroup per (kv head, tile of 64 positions): the
+// tile's K and V rows are staged in LDS with one coalesced load round, the G
+// query heads sharing the kv head (GQA) score all 64 positions in parallel,
+// and each head's tile partial (running max m, sum l, unnormalized P*V) goes
+// to global memory.  The workgroup that finishes last for a kv head (device
+// fence + atomic counter) merges the tiles with the log-sum-exp rule, writes
+// the attention output and, for the integer path, its Q8_0 blocks (the
+// reference quantizes this row inside the o-projection's `linear`,
+// src/kernels/matmul.rs:91-98).  Tiles beyond the current length exit at
+// once, so one launch shape serves every position of a captured graph.
+constexpr int TP = 64;  // positions per tile
+
 template <int G>
-__global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q,
-                                                          const float* __restrict__ kc,
-                                                          const float* __restrict__ vc,
-                                                          const int* __restrict__ pos_ptr,
-                                                          int n_kv_heads, int nsplit, float* part_m,
-                                                          float* part_l, float* part_o) {
+__global__ __launch_bounds__(256) void attn_decode_kernel(
+    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    const int* __restrict__ pos_ptr, int n_kv_heads, int max_tiles, float* part_m, float* part_l,
+    float* part_o, unsigned* counters, float* attn, int8_t* act_q, uint16_t* act_d) {
+    __shared__ float s_k[TP][HD + 1];
+    __shared__ __attribute__((aligned(16))) float s_v[TP][HD];
     __shared__ float s_q[G][HD];
-    __shared__ float s_p[G][64];
+    __shared__ float s_p[G][TP];
+    __shared__ float s_m[G], s_l[G];
+    __shared__ int s_last;
     const int g = blockIdx.x;
-    const int sp = blockIdx.y;
-    const int lane = threadIdx.x;
+    const int tile = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int P = *pos_ptr + 1;
+    const int ntiles = (P + TP - 1) / TP;
+    if (tile >= ntiles) return;
     const int kv_dim = n_kv_heads * HD;
+    const int s0 = tile * TP;
     const float scale = 1.0f / sqrtf((float)HD);
 
-#pragma unroll
-    for (int i = 0; i < G; i++) s_q[i][lane] = q[(g * G + i) * HD + lane];
+    for (int e = tid; e < TP * HD / 4; e += 256) {
+        const int r = e / (HD / 4), c4 = e % (HD / 4);
+        float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
+        if (s0 + r < P) {
+            const size_t off = (size_t)(s0 + r) * kv_dim + g * HD + 4 * c4;
+            k4 = *(const float4*)(kc + off);
+            v4 = *(const float4*)(vc + off);
+        }
+        s_k[r][4 * c4 + 0] = k4.x;
+        s_k[r][4 * c4 + 1] = k4.y;
+        s_k[r][4 * c4 + 2] = k4.z;
+        s_k[r][4 * c4 + 3] = k4.w;
+        *(float4*)&s_v[r][4 * c4] = v4;
+    }
+    for (int e = tid; e < G * HD; e += 256) s_q[e / HD][e % HD] = q[(size_t)g * G * HD + e];
     __syncthreads();
 
-    float m[G], l[G], acc[G];
-#pragma unroll
-    for (int i = 0; i < G; i++) {
-        m[i] = -INFINITY;
-        l[i] = 0.0f;
-        acc[i] = 0.0f;
+    // scores = dot(q, k) * (1/sqrt(head_dim)) (attention.rs:52-55)
+    for (int idx = tid; idx < G * TP; idx += 256) {
+        const int i = idx / TP, sp = idx % TP;
+        float dot = 0.0f;
+#pragma unroll 16
+        for (int d = 0; d < HD; d++) dot += s_q[i][d] * s_k[sp][d];
+        s_p[i][sp] = (s0 + sp < P) ? dot * scale : -INFINITY;
     }
-
-    for (int tile = sp; tile * 64 < P; tile += nsplit) {
-        const int s = tile * 64 + lane;
-        const bool valid = s < P;
-        float sc[G];
-        if (valid) {
-            const float4* kr = (const float4*)(kc + (size_t)s * kv_dim + g * HD);
-            float4 k4[HD / 4];
-#pragma unroll
-            for (int d = 0; d < HD / 4; d++) k4[d] = kr[d];
-#pragma unroll
-            for (int i = 0; i < G; i++) {
-                float dot = 0.0f;
-#pragma unroll
-                for (int d = 0; d < HD / 4; d++) {
-                    dot += s_q[i][4 * d + 0] * k4[d].x;
-                    dot += s_q[i][4 * d + 1] * k4[d].y;
-                    dot += s_q[i][4 * d + 2] * k4[d].z;
-                    dot += s_q[i][4 * d + 3] * k4[d].w;
-                }
-                sc[i] = dot * scale;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < G; i++) sc[i] = -INFINITY;
-        }
-#pragma unroll
-        for (int i = 0; i < G; i++) {
-            const float tmax = sq_wave_max(sc[i]);
-            const float mn = fmaxf(m[i], tmax);
-            const float alpha = (m[i] == -INFINITY) ? 0.0f : expf(m[i] - mn);
-            const float p = valid ? expf(sc[i] - mn) : 0.0f;
-            l[i] = l[i] * alpha + sq_wave_sum(p);
-            acc[i] *= alpha;
-            m[i] = mn;
-            s_p[i][lane] = p;
-        }
-        __syncthreads();
-        const int nvalid = min(64, P - tile * 64);
-        const float* vbase = vc + (size_t)tile * 64 * kv_dim + g * HD + lane;
-        for (int j = 0; j < nvalid; j++) {
-            const float v = vbase[(size_t)j * kv_dim];
-#pragma unroll
-            for (int i = 0; i < G; i++) acc[i] += s_p[i][j] * v;
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < G; i++) {
-        const int idx = (g * G + i) * nsplit + sp;
+    __syncthreads();
+    for (int i = wave; i < G; i += 4) {
+        const float v = s_p[i][lane];
+        const float m = sq_wave_max(v);
+        const float p = (v == -INFINITY) ? 0.0f : expf(v - m);
+        const float l = sq_wave_sum(p);
+        s_p[i][lane] = p;
         if (lane == 0) {
-            part_m[idx] = m[i];
-            part_l[idx] = l[i];
+            s_m[i] = m;
+            s_l[i] = l;
         }
-        part_o[(size_t)idx * HD + lane] = acc[i];
     }
-}
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += 256) {
+        const int i = idx / HD, d = idx % HD;
+        float o = 0.0f;
+#pragma unroll 16
+        for (int sp = 0; sp < TP; sp++) o += s_p[i][sp] * s_v[sp][d];
+        const int pidx = (g * G + i) * max_tiles + tile;
+        part_o[(size_t)pidx * HD + d] = o;
+        if (d == 0) {
+            part_m[pidx] = s_m[i];
+            part_l[pidx] = s_l[i];
+        }
+    }
 
-// Merge the splits of one head; lane = dimension.  Optionally quantizes the
-// head's two 32-blocks for the o-projection (the reference quantizes the
-// attention output row inside `linear`, src/kernels/matmul.rs:91-98).
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float* part_m, const float* part_l,
-                                                           const float* part_o, int nsplit,
-                                                           float* attn, int8_t* act_q,
-                                                           uint16_t* act_d) {
-    const int h = blockIdx.x;
-    const int lane = threadIdx.x;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, part_m[h * nsplit + s]);
-    float L = 0.0f, O = 0.0f;
-    for (int s = 0; s < nsplit; s++) {
-        const float ms = part_m[h * nsplit + s];
-        if (ms == -INFINITY) continue;
-        const float e = expf(ms - M);
-        L += part_l[h * nsplit + s] * e;
-        O += part_o[(size_t)(h * nsplit + s) * HD + lane] * e;
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        const unsigned prev = atomicAdd(&counters[g], 1u);
+        s_last = prev == (unsigned)(ntiles - 1);
     }
-    const float out = O / L;
-    attn[h * HD + lane] = out;
-    if (act_q) {
-        float amax = fmaxf(sq_half_max(fabsf(out)), 0.0f);
-        float scale = sq_q8_scale(amax);
-        float inv = sq_q8_inv(scale);
-        act_q[h * HD + lane] = sq_q8_quant(out, inv);
-        if ((lane & 31) == 0) act_d[(h * HD + lane) >> 5] = sq_f32_to_f16(scale);
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int idx = tid; idx < G * HD; idx += 256) {
+        const int i = idx / HD, d = idx % HD, h = g * G + i;
+        float M = -INFINITY;
+        for (int t = 0; t < ntiles; t++) M = fmaxf(M, part_m[h * max_tiles + t]);
+        float L = 0.0f, O = 0.0f;
+        for (int t = 0; t < ntiles; t++) {
+            const int pidx = h * max_tiles + t;
+            const float mt = part_m[pidx];
+            if (mt == -INFINITY) continue;
+            const float e = expf(mt - M);
+            L += part_l[pidx] * e;
+            O += part_o[(size_t)pidx * HD + d] * e;
+        }
+        const float out = O / L;
+        attn[h * HD + d] = out;
+        if (act_q) {
+            const float amax = fmaxf(sq_half_max(fabsf(out)), 0.0f);
+            const float sc = sq_q8_scale(amax);
+            const float inv = sq_q8_inv(sc);
+            act_q[h * HD + d] = sq_q8_quant(out, inv);
+            if ((d & 31) == 0) act_d[(h * HD + d) >> 5] = sq_f32_to_f16(sc);
+        }
     }
+    if (tid == 0) atomicExch(&counters[g], 0u);
 }
 
 // Prefill attention: 64 query rows of one head per workgroup, K/V tiles of
@@ -318,29 +318,24 @@ __global__ __launch_bounds__(64) void sdpa_generic_kernel(const float* q, const 
 
 }  // namespace
 
-int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const float* vcache,
-                       const int* pos, int n_heads, int n_kv_heads, int head_dim, int nsplit,
-                       float* part_m, float* part_l, float* part_o) {
+int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const float* vcache, const int* pos,
+                       int n_heads, int n_kv_heads, int head_dim, int max_tiles, float* part_m, float* part_l,
+                       float* part_o, unsigned* counters, float* attn, int8_t* act_q, uint16_t* act_d) {
     if (head_dim != HD) return set_error(SQ_ERR_UNSUPPORTED, "attention kernels are built for head_dim 64");
     const int G = n_heads / n_kv_heads;
-    dim3 grid(n_kv_heads, nsplit);
+    dim3 grid(n_kv_heads, max_tiles);
+#define SQ_ATTN_LAUNCH(GG)                                                                                      \
+    hipLaunchKernelGGL(attn_decode_kernel<GG>, grid, dim3(256), 0, s, q, kcache, vcache, pos, n_kv_heads,      \
+                       max_tiles, part_m, part_l, part_o, counters, attn, act_q, act_d)
     switch (G) {
-        case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(64), 0, s, q, kcache, vcache, pos, n_kv_heads, nsplit, part_m, part_l, part_o); break;
-        case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(64), 0, s, q, kcache, vcache, pos, n_kv_heads, nsplit, part_m, part_l, part_o); break;
-        case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(64), 0, s, q, kcache, vcache, pos, n_kv_heads, nsplit, part_m, part_l, part_o); break;
-        case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(64), 0, s, q, kcache, vcache, pos, n_kv_heads, nsplit, part_m, part_l, part_o); break;
+        case 1: SQ_ATTN_LAUNCH(1); break;
+        case 2: SQ_ATTN_LAUNCH(2); break;
+        case 4: SQ_ATTN_LAUNCH(4); break;
+        case 8: SQ_ATTN_LAUNCH(8); break;
         default: return set_error(SQ_ERR_UNSUPPORTED, "GQA group size must be 1, 2, 4 or 8");
     }
+#undef SQ_ATTN_LAUNCH
     return check_launch("attn_decode");
-}
-
-int launch_attn_combine(hipStream_t s, const float* part_m, const float* part_l, const float* part_o,
-                        int n_heads, int head_dim, int nsplit, float* attn, int8_t* act_q,
-                        uint16_t* act_d) {
-    if (head_dim != HD) return set_error(SQ_ERR_UNSUPPORTED, "attention kernels are built for head_dim 64");
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(64), 0, s, part_m, part_l, part_o, nsplit,
-                       attn, act_q, act_d);
-    return check_launch("attn_combine");
 }
 
 int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, const float* vcache, int pos0,

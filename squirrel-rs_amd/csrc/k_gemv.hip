@@ -4,9 +4,14 @@
 // slot).  Lane L of a wavefront owns weight blocks L, L+64, ... of every row
 // it processes, so a wavefront reads each row as contiguous 2 KB segments
 // (Q8_0 payload) with 16-byte loads, and the lane's activation blocks stay in
-// registers for every row.  Each wavefront keeps R rows in flight; the first
-// tile's weights are requested before the prologue (the activations never
-// gate the weight stream), and later tiles are prefetched one tile ahead.
+// registers for every row.  Each wavefront keeps R rows in flight.
+//
+// Load ordering matters on CDNA: a wavefront's loads complete in issue order,
+// so the prologue's inputs (the hidden row, norm gains, the RoPE position)
+// are requested first, the first tile's weights right after them, and the
+// prologue arithmetic then runs while the weight stream is in flight.  With
+// a grid smaller than the tile count, later tiles are prefetched one tile
+// ahead into a second register buffer.
 //
 // Arithmetic per weight block follows the reference:
 //   A8 (integer path, src/kernels/dot_prod.rs:378-403):
@@ -41,6 +46,24 @@ struct Gemv {
     static constexpr int DW = WBlk<WT>::DW;
     static constexpr int EPT = (KMAX + NT - 1) / NT;  // prologue elements per thread
 };
+
+// Dequantized element i of embedding row `tok` (dequantize_into,
+// src/kernels/dot_prod.rs:409-414, 440-446, 524-528): exact.
+__device__ __forceinline__ float embed_elem(const MatView& t, uint32_t tok, int i) {
+    const int K = t.k, KB = K >> 5;
+    const int blk = i >> 5, j = i & 31;
+    if (t.wtype == WT_Q8_0) {
+        const float sc = sq_f16_to_f32(t.scale[(size_t)tok * KB + blk]);
+        return sc * (float)((const int8_t*)t.qs)[(size_t)tok * K + i];
+    }
+    if (t.wtype == WT_Q4_0) {
+        const uint8_t* qs = (const uint8_t*)t.qs + (size_t)tok * (K / 2) + blk * 16;
+        const float sc = sq_f16_to_f32(t.scale[(size_t)tok * KB + blk]);
+        const int q = j < 16 ? (qs[j] & 0x0F) : (qs[j - 16] >> 4);
+        return sc * (float)(q - 8);
+    }
+    return sq_bf16_to_f32(((const uint16_t*)t.qs)[(size_t)tok * K + i]);
+}
 
 template <int WT, bool A8, int NBL, int R, int WAVES, int PRO, int EPI, int NBUF>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
@@ -121,24 +144,61 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     };
 
     int t = blockIdx.x;
-    if (t < n_tiles) load_tile(W0, D0, t);
 
-    // ---------------------------------------------------------------- prologue
+    // ------------------------------------------------- prologue loads first
+    float xv[PRO == PRO_NORM ? G::EPT : 1];
+    float nw[PRO == PRO_NORM ? G::EPT : 1];
     int AQ[NBL][8];
     float AS[NBL];
     int ASUM[NBL];
     if constexpr (PRO == PRO_NORM) {
-        // rms_norm_f32_into (src/kernels/rms_norm.rs:40-56): ss = sum x^2,
-        // rms = sqrt(ss/n + eps), y = (x*w)/rms.
-        float xv[G::EPT];
-        float ss = 0.0f;
+        const bool from_embed = a.embd.qs != nullptr;
+        const uint32_t tok = from_embed ? min(*a.token, (uint32_t)(a.embd.rows - 1)) : 0u;
 #pragma unroll
         for (int j = 0; j < G::EPT; j++) {
             const int i = tid + j * G::NT;
-            float x = (i < K) ? a.x[i] : 0.0f;
-            xv[j] = x;
-            ss += x * x;
+            const bool vi = i < K;
+            xv[j] = vi ? (from_embed ? embed_elem(a.embd, tok, i) : a.x[i]) : 0.0f;
+            nw[j] = vi ? a.norm_w[i] : 0.0f;
         }
+    } else if constexpr (PRO == PRO_Q8) {
+#pragma unroll
+        for (int b = 0; b < NBL; b++) {
+            const int blk = lane + 64 * b;
+            if (blk < KB) {
+                const int4* p = (const int4*)(a.aq + blk * 32);
+                int4 x0 = p[0], x1 = p[1];
+                AQ[b][0] = x0.x; AQ[b][1] = x0.y; AQ[b][2] = x0.z; AQ[b][3] = x0.w;
+                AQ[b][4] = x1.x; AQ[b][5] = x1.y; AQ[b][6] = x1.z; AQ[b][7] = x1.w;
+                AS[b] = sq_f16_to_f32(a.ad[blk]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 8; v++) AQ[b][v] = 0;
+                AS[b] = 0.0f;
+            }
+            ASUM[b] = 0;
+        }
+    }
+    // The RoPE position, read before the weight stream is requested.
+    int qkv_pos = 0;
+    if constexpr (EPI == EPI_QKV) qkv_pos = *a.pos;
+
+    if (t < n_tiles) load_tile(W0, D0, t);
+
+    // ---------------------------------------------------- prologue compute
+    if constexpr (PRO == PRO_NORM) {
+        // rms_norm_f32_into (src/kernels/rms_norm.rs:40-56): ss = sum x^2,
+        // rms = sqrt(ss/n + eps), y = (x*w)/rms.
+        if (a.embd.qs != nullptr && blockIdx.x == 0) {
+#pragma unroll
+            for (int j = 0; j < G::EPT; j++) {
+                const int i = tid + j * G::NT;
+                if (i < K) a.hidden_out[i] = xv[j];
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < G::EPT; j++) ss += xv[j] * xv[j];
         ss = sq_wave_sum(ss);
         if (lane == 0) s_red[wave] = ss;
         __syncthreads();
@@ -152,7 +212,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         for (int j = 0; j < G::EPT; j++) {
             const int i = tid + j * G::NT;
             const bool vi = i < K;
-            float y = vi ? (xv[j] * a.norm_w[i]) / rms : 0.0f;
+            float y = vi ? (xv[j] * nw[j]) / rms : 0.0f;
             if constexpr (A8) {
                 float amax = fmaxf(sq_half_max(fabsf(y)), 0.0f);
                 float scale = sq_q8_scale(amax);
@@ -199,26 +259,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             }
         }
     } else if constexpr (PRO == PRO_Q8) {
+        if constexpr (WT == WT_Q4_0) {
 #pragma unroll
-        for (int b = 0; b < NBL; b++) {
-            const int blk = lane + 64 * b;
-            if (blk < KB) {
-                const int4* p = (const int4*)(a.aq + blk * 32);
-                int4 x0 = p[0], x1 = p[1];
-                AQ[b][0] = x0.x; AQ[b][1] = x0.y; AQ[b][2] = x0.z; AQ[b][3] = x0.w;
-                AQ[b][4] = x1.x; AQ[b][5] = x1.y; AQ[b][6] = x1.z; AQ[b][7] = x1.w;
-                AS[b] = sq_f16_to_f32(a.ad[blk]);
-                if constexpr (WT == WT_Q4_0) {
-                    int sacc = 0;
+            for (int b = 0; b < NBL; b++) {
+                int sacc = 0;
 #pragma unroll
-                    for (int v = 0; v < 8; v++) sacc = __builtin_amdgcn_sdot4(AQ[b][v], 0x01010101, sacc, false);
-                    ASUM[b] = sacc;
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < 8; v++) AQ[b][v] = 0;
-                AS[b] = 0.0f;
-                ASUM[b] = 0;
+                for (int v = 0; v < 8; v++) sacc = __builtin_amdgcn_sdot4(AQ[b][v], 0x01010101, sacc, false);
+                ASUM[b] = sacc;
             }
         }
     } else {  // PRO_F32
@@ -320,7 +367,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
                 }
             }
         } else if constexpr (EPI == EPI_QKV) {
-            const int p = *a.pos;
+            const int p = qkv_pos;
 #pragma unroll
             for (int r = 0; r < R; r += 2) {
                 const int row = t * TR + wave * R + r;
@@ -374,6 +421,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             __syncthreads();
         }
     };
+
     if constexpr (NBUF == 2) {
         // Grid-stride over tiles with the next tile's weights in flight.
         while (t < n_tiles) {
@@ -393,40 +441,42 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     }
 
     if constexpr (EPI == EPI_LOGITS) {
-        // Reduce (value, index) with the reference's rule: larger value wins,
+        // (value, index) with the reference's rule: the larger value wins,
         // equal values go to the larger index (Iterator::max_by keeps the
         // last maximum, src/samplers/greedy.rs:8-13).  NaN rows are tracked
-        // separately; the final pass resolves them.
+        // separately and resolved by the last workgroup.
+        auto merge = [](float& bv, int& bi, int& bn, float v, int i, int n) {
+            if (i >= 0 && (bi < 0 || v > bv || (v == bv && i > bi))) {
+                bv = v;
+                bi = i;
+            }
+            bn = n > bn ? n : bn;
+        };
+        auto block_merge = [&](float& bv, int& bi, int& bn) {
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            float ov = __shfl_xor(best_v, o, 64);
-            int oi = __shfl_xor(best_i, o, 64);
-            int on = __shfl_xor(nan_i, o, 64);
-            if (oi >= 0 && (best_i < 0 || ov > best_v || (ov == best_v && oi > best_i))) {
-                best_v = ov;
-                best_i = oi;
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                const int on = __shfl_xor(bn, o, 64);
+                merge(bv, bi, bn, ov, oi, on);
             }
-            nan_i = on > nan_i ? on : nan_i;
-        }
-        if (lane == 0) {
-            s_bv[wave] = best_v;
-            s_bi[wave] = best_i;
-            s_bn[wave] = nan_i;
-        }
-        __syncthreads();
+            __syncthreads();
+            if (lane == 0) {
+                s_bv[wave] = bv;
+                s_bi[wave] = bi;
+                s_bn[wave] = bn;
+            }
+            __syncthreads();
+            bv = s_bv[0];
+            bi = s_bi[0];
+            bn = s_bn[0];
+            for (int w = 1; w < WAVES; w++) merge(bv, bi, bn, s_bv[w], s_bi[w], s_bn[w]);
+        };
+        block_merge(best_v, best_i, nan_i);
         if (tid == 0) {
-            float bv = s_bv[0];
-            int bi = s_bi[0], bn = s_bn[0];
-            for (int w = 1; w < WAVES; w++) {
-                if (s_bi[w] >= 0 && (bi < 0 || s_bv[w] > bv || (s_bv[w] == bv && s_bi[w] > bi))) {
-                    bv = s_bv[w];
-                    bi = s_bi[w];
-                }
-                bn = s_bn[w] > bn ? s_bn[w] : bn;
-            }
-            a.part_val[blockIdx.x] = bv;
-            a.part_idx[blockIdx.x] = bi;
-            a.part_nan[blockIdx.x] = bn;
+            a.part_val[blockIdx.x] = best_v;
+            a.part_idx[blockIdx.x] = best_i;
+            a.part_nan[blockIdx.x] = nan_i;
         }
     }
 }
@@ -464,7 +514,7 @@ int dispatch(hipStream_t s, int pro, int epi, const GemvArgs& a, int* grid_out) 
                 return run<WT, A8, 1, 8, 8, PRO_NORM, EPI_GATEUP>(s, a, 1 << 30, grid_out);
         case EPI_LOGITS:
             if (pro != PRO_NORM || KB > 64) break;
-            return run<WT, A8, 1, 4, 4, PRO_NORM, EPI_LOGITS, 2>(s, a, 1024, grid_out);
+            return run<WT, A8, 1, 4, 4, PRO_NORM, EPI_LOGITS, 2>(s, a, kLogitsGrid, grid_out);
         case EPI_RESID:
             if (pro != PRO_A) break;
             if (KB <= 64) return run<WT, A8, 1, 2, 4, PRO_A, EPI_RESID>(s, a, 1 << 30, grid_out);
@@ -489,6 +539,8 @@ int launch_gemv(hipStream_t s, int pro, int epi, bool a8, const GemvArgs& a, int
         return set_error(SQ_ERR_SHAPE, "gemv: k must be a positive multiple of 32");
     if (epi == EPI_GATEUP && a.n_rows % 32 != 0)
         return set_error(SQ_ERR_SHAPE, "gemv: gate/up width must be a multiple of 32");
+    if (a.embd.qs != nullptr && (a.token == nullptr || a.hidden_out == nullptr || a.embd.k != a.w.k))
+        return set_error(SQ_ERR_ARG, "gemv: embedding prologue needs a token, a hidden output and k = dim");
     switch (a.w.wtype) {
         case WT_Q8_0:
             return a8 ? dispatch<WT_Q8_0, true>(s, pro, epi, a, grid_out)

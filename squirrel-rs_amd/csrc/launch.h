@@ -20,6 +20,9 @@ enum GemvEpi : int {
     EPI_LOGITS = 4,  // logits[row] = v, per-workgroup argmax partials
 };
 
+// Workgroups of the LM-head matvec; its argmax partials have this many slots.
+constexpr int kLogitsGrid = 1024;
+
 struct GemvArgs {
     MatView w;
     int n_rows;        // logical output rows (EPI_GATEUP: ffn width)
@@ -43,6 +46,11 @@ struct GemvArgs {
     float* part_val;       // EPI_LOGITS
     int* part_idx;
     int* part_nan;
+    // PRO_NORM from the embedding table: x = dequantized row *token of embd
+    // (when embd.qs is non-null); workgroup 0 also stores x to hidden_out.
+    MatView embd;
+    const uint32_t* token;
+    float* hidden_out;
     // debug taps of the prologue (workgroup 0 only, when non-null)
     float* dbg_normed;
     int8_t* dbg_qs;
@@ -54,15 +62,15 @@ struct GemvArgs {
 int launch_gemv(hipStream_t s, int pro, int epi, bool a8, const GemvArgs& a, int* grid_out);
 
 // ---- attention (k_attn.hip) ------------------------------------------------
-// Decode: one query row per head at position *pos, keys 0..*pos (inclusive).
+// Decode: one query row per head at position *pos, keys 0..*pos (inclusive),
+// tiles of 64 positions (grid n_kv_heads x max_tiles).  Writes attn f32 and,
+// when act_q is non-null, Q8_0 blocks of each head's output.  part_* hold
+// n_heads * max_tiles partials; counters (n_kv_heads) must start at zero and
+// are left at zero.
 int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const float* vcache,
-                       const int* pos, int n_heads, int n_kv_heads, int head_dim, int nsplit,
-                       float* part_m, float* part_l, float* part_o);
-// Merge the split partials; writes attn f32 and, when act_q != null, Q8_0
-// blocks of each head's output (the o-projection's quantized input).
-int launch_attn_combine(hipStream_t s, const float* part_m, const float* part_l,
-                        const float* part_o, int n_heads, int head_dim, int nsplit, float* attn,
-                        int8_t* act_q, uint16_t* act_d);
+                       const int* pos, int n_heads, int n_kv_heads, int head_dim, int max_tiles,
+                       float* part_m, float* part_l, float* part_o, unsigned* counters, float* attn,
+                       int8_t* act_q, uint16_t* act_d);
 // Prefill: m query rows at positions pos0 .. pos0+m-1 against keys 0..pos0+m-1.
 int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, const float* vcache,
                         int pos0, int m, int n_heads, int n_kv_heads, int head_dim,

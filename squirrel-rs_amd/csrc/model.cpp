@@ -429,11 +429,11 @@ int build_decode_step(sq_ctx* c) {
     std::vector<std::function<int()>> step;
     std::vector<int> named(K_COUNT, -1);
 
-    const MatView embd = view(m->embd);
-    const int wt = m->wtype;
-    step.push_back([=]() { return launch_embed(s, embd, wt, c->d_token, 1, D, c->hidden); });
     const size_t kv_layer = c->max_pos * (size_t)KVD;
     auto mat_bytes = [](const DevMatrix& x) { return (uint64_t)(x.payload_bytes() + x.scale_bytes()); };
+    // Kernels replayed by the measurement entry point come from layer 1 (layer
+    // 0's QKV also performs the embedding lookup).
+    const int lt = g.n_layers > 1 ? 1 : 0;
     for (int l = 0; l < g.n_layers; l++) {
         const Layer& Ly = m->layers[l];
         float* kc = c->kcache + l * kv_layer;
@@ -453,26 +453,27 @@ int build_decode_step(sq_ctx* c) {
         q.kv_rows = KVD;
         q.half = g.head_dim / 2;
         if (l == 0) {
+            // embed (model.rs:57-62) fused into the first norm prologue
+            q.embd = view(m->embd);
+            q.token = c->d_token;
+            q.hidden_out = c->hidden;
             q.dbg_normed = c->dbg_normed;
             q.dbg_qs = c->dbg_qs;
             q.dbg_d = c->dbg_d;
         }
-        if (l == 0) {
+        if (l == lt) {
             named[K_QKV] = (int)step.size();
             c->kernel_bytes[K_QKV] = mat_bytes(Ly.qkv) + 2ull * D * 4 + (uint64_t)(QD + 2 * KVD) * 4;
         }
         step.push_back([=]() { return launch_gemv(s, PRO_NORM, EPI_QKV, a8, q, nullptr); });
-        if (l == 0) {
+        if (l == lt) {
             named[K_ATTN] = (int)step.size();
             c->kernel_bytes[K_ATTN] = 0;  // depends on the position; filled at measurement time
         }
         step.push_back([=]() {
-            return launch_attn_decode(s, c->q, kc, vc, c->d_pos, g.n_heads, g.n_kv_heads, g.head_dim, c->nsplit,
-                                      c->part_m, c->part_l, c->part_o);
-        });
-        step.push_back([=]() {
-            return launch_attn_combine(s, c->part_m, c->part_l, c->part_o, g.n_heads, g.head_dim, c->nsplit,
-                                       c->attn, a8 ? c->attn_q : nullptr, c->attn_d);
+            return launch_attn_decode(s, c->q, kc, vc, c->d_pos, g.n_heads, g.n_kv_heads, g.head_dim, c->max_tiles,
+                                      c->part_m, c->part_l, c->part_o, c->attn_counters, c->attn,
+                                      a8 ? c->attn_q : nullptr, c->attn_d);
         });
         GemvArgs o{};
         o.w = view(Ly.o);
@@ -481,7 +482,7 @@ int build_decode_step(sq_ctx* c) {
         o.ad = c->attn_d;
         o.x = c->attn;
         o.out = c->hidden;
-        if (l == 0) {
+        if (l == lt) {
             named[K_OPROJ] = (int)step.size();
             c->kernel_bytes[K_OPROJ] = mat_bytes(Ly.o) + (a8 ? (uint64_t)QD + QD / 16 : (uint64_t)QD * 4) + 2ull * D * 4;
         }
@@ -495,7 +496,7 @@ int build_decode_step(sq_ctx* c) {
         gu.ffn_act = c->ffn_act;
         gu.act_q = a8 ? c->ffn_q : nullptr;
         gu.act_d = c->ffn_d;
-        if (l == 0) {
+        if (l == lt) {
             named[K_GATEUP] = (int)step.size();
             c->kernel_bytes[K_GATEUP] = mat_bytes(Ly.gateup) + 2ull * D * 4 + (uint64_t)F * 4 +
                                         (a8 ? (uint64_t)F + F / 16 : 0);
@@ -508,7 +509,7 @@ int build_decode_step(sq_ctx* c) {
         dn.ad = c->ffn_d;
         dn.x = c->ffn_act;
         dn.out = c->hidden;
-        if (l == 0) {
+        if (l == lt) {
             named[K_DOWN] = (int)step.size();
             c->kernel_bytes[K_DOWN] = mat_bytes(Ly.down) + (a8 ? (uint64_t)F + F / 16 : (uint64_t)F * 4) + 2ull * D * 4;
         }
@@ -645,9 +646,8 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
     int st;
     hipError_t he = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (he != hipSuccess) return fail(set_error(SQ_ERR_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(he)));
-    const size_t tiles = (max_pos + 63) / 64;
-    c->nsplit = (int)std::min<size_t>(64, std::max<size_t>(1, (tiles + 1) / 2));
-    c->n_parts = 1024;
+    c->max_tiles = (int)((max_pos + 63) / 64);
+    c->n_parts = kLogitsGrid;
     if ((st = dmalloc(&c->kcache, (size_t)g.n_layers * max_pos * KVD)) ||
         (st = dmalloc(&c->vcache, (size_t)g.n_layers * max_pos * KVD)) || (st = dmalloc(&c->rope, max_pos * half)) ||
         (st = dmalloc(&c->d_pos, 1)) || (st = dmalloc(&c->d_token, 1)) || (st = dmalloc(&c->d_ids, max_pos)) ||
@@ -655,9 +655,11 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
         (st = dmalloc(&c->q, QD)) || (st = dmalloc(&c->attn, QD)) || (st = dmalloc(&c->attn_q, QD)) ||
         (st = dmalloc(&c->attn_d, QD / 32)) || (st = dmalloc(&c->ffn_act, F)) || (st = dmalloc(&c->ffn_q, F)) ||
         (st = dmalloc(&c->ffn_d, F / 32)) || (st = dmalloc(&c->logits, (size_t)g.vocab)) ||
-        (st = dmalloc(&c->part_m, (size_t)g.n_heads * c->nsplit)) ||
-        (st = dmalloc(&c->part_l, (size_t)g.n_heads * c->nsplit)) ||
-        (st = dmalloc(&c->part_o, (size_t)g.n_heads * c->nsplit * g.head_dim)) || (st = dmalloc(&c->pv, c->n_parts)) ||
+        (st = dmalloc(&c->part_m, (size_t)g.n_heads * c->max_tiles)) ||
+        (st = dmalloc(&c->part_l, (size_t)g.n_heads * c->max_tiles)) ||
+        (st = dmalloc(&c->part_o, (size_t)g.n_heads * c->max_tiles * g.head_dim)) ||
+        (st = dmalloc(&c->attn_counters, (size_t)g.n_kv_heads)) ||
+        (st = dmalloc(&c->pv, c->n_parts)) ||
         (st = dmalloc(&c->pi, c->n_parts)) || (st = dmalloc(&c->pn, c->n_parts)) ||
         (st = dmalloc(&c->dbg_normed, D)) || (st = dmalloc(&c->dbg_qs, D)) || (st = dmalloc(&c->dbg_d, D / 32)) ||
         (st = dmalloc(&c->last_hidden, D)) || (st = dmalloc(&c->head_qs, D)) || (st = dmalloc(&c->head_d, D / 32)))
@@ -680,6 +682,7 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
     SQ_HIP_CHECK(hipMemcpy(c->pv, init_v.data(), c->n_parts * 4, hipMemcpyHostToDevice));
     SQ_HIP_CHECK(hipMemcpy(c->pi, init_i.data(), c->n_parts * 4, hipMemcpyHostToDevice));
     SQ_HIP_CHECK(hipMemcpy(c->pn, init_i.data(), c->n_parts * 4, hipMemcpyHostToDevice));
+    SQ_HIP_CHECK(hipMemset(c->attn_counters, 0, (size_t)g.n_kv_heads * 4));
     SQ_HIP_CHECK(hipMemset(c->d_pos, 0, 4));
     SQ_HIP_CHECK(hipMemset(c->d_nhist, 0, 4));
     SQ_HIP_CHECK(hipMemset(c->d_token, 0, 4));
@@ -711,7 +714,7 @@ void ctx_destroy(sq_ctx* c) {
     dfree(c->kcache); dfree(c->vcache); dfree(c->rope); dfree(c->d_pos); dfree(c->d_token); dfree(c->d_ids);
     dfree(c->d_hist); dfree(c->d_nhist); dfree(c->hidden); dfree(c->q); dfree(c->attn); dfree(c->attn_q);
     dfree(c->attn_d); dfree(c->ffn_act); dfree(c->ffn_q); dfree(c->ffn_d); dfree(c->logits); dfree(c->part_m);
-    dfree(c->part_l); dfree(c->part_o); dfree(c->pv); dfree(c->pi); dfree(c->pn); dfree(c->dbg_normed);
+    dfree(c->part_l); dfree(c->part_o); dfree(c->attn_counters); dfree(c->pv); dfree(c->pi); dfree(c->pn); dfree(c->dbg_normed);
     dfree(c->dbg_qs); dfree(c->dbg_d); dfree(c->last_hidden); dfree(c->head_qs); dfree(c->head_d);
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
     dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad);
@@ -832,6 +835,8 @@ int ctx_generate(sq_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t max_
 
 int ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes) {
     if (which < 0 || which >= K_COUNT || iters <= 0) return set_error(SQ_ERR_ARG, "time_kernel: bad kernel id");
+    // Replays write the KV row at the current position and attend up to it.
+    if (c->seq_len >= c->max_pos) return set_error(SQ_ERR_CACHE_FULL, "time_kernel: KV cache is full");
     const Config& g = c->m->cfg;
     hipEvent_t e0, e1;
     SQ_HIP_CHECK(hipEventCreate(&e0));
@@ -850,7 +855,7 @@ int ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* 
     *mean_us = 1000.0 * ms / iters;
     uint64_t b = c->kernel_bytes[which];
     if (which == K_ATTN) {
-        const uint64_t P = c->seq_len;  // positions attended by a replay at the current position
+        const uint64_t P = c->seq_len + 1;  // positions attended by a replay at the current position
         b = 2ull * P * g.n_kv_heads * g.head_dim * 4 + (uint64_t)g.n_heads * g.head_dim * 4;
     }
     if (bytes) *bytes = b;

@@ -84,7 +84,8 @@ struct sq_ctx {
     uint16_t* ffn_d = nullptr;
     float* logits = nullptr;
     float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
-    int nsplit = 0;
+    int max_tiles = 0;               // 64-position attention tiles of max_pos
+    unsigned* attn_counters = nullptr;  // one per kv head, zero between launches
     float* pv = nullptr;
     int* pi = nullptr;
     int* pn = nullptr;

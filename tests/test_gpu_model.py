@@ -14,8 +14,15 @@ aarch64 NEON combine order vs its scalar twin) therefore either agree to
 error (measured on these models, 8 seeds).  The bar for the GPU is the same:
 per step, the relative L2 error of the GPU logits against the oracle's W8A8
 logits must not exceed the reference's own W8A8-vs-W8A32 relative L2 error on
-the same inputs (REL_TOL_FACTOR x that gap).  Integer parity itself is pinned
-bit for bit at the kernel level (quantizer, block sums, fused norm+quantize).
+the same inputs.  Two bars follow from that:
+  * the GPU's W8A8 logits are as close to the f32-activation (W8A32) logits as
+    the oracle's W8A8 logits are: rel_l2(gpu, W8A32) <= F32_FACTOR * gap;
+  * the GPU and the oracle differ by no more than two independent W8A8
+    roundings would: rel_l2(gpu, W8A8) <= PAIR_FACTOR * gap (sqrt(2) plus
+    margin).
+Where no flip happens the two agree to f32 rounding (~1e-7 relative; printed).
+Integer parity itself is pinned bit for bit at the kernel level (quantizer,
+block sums, fused norm+quantize).
 """
 import os
 
@@ -28,7 +35,8 @@ pytestmark = pytest.mark.gpu
 
 sq = pytest.importorskip("sqhip")
 
-REL_TOL_FACTOR = 1.0
+F32_FACTOR = 1.25
+PAIR_FACTOR = 1.5
 LOGIT_ABS_FLOOR = 2e-4
 MODES = {"Q8_0": O.W8A8, "Q4_0": O.W8A8, "BF16": O.W8A32}
 A32_SKIP = ("f32-activation kernels (BF16, SQUIRREL_F32_ACTS) are switched off after a GPU "
@@ -77,13 +85,15 @@ def check_logits(path, seq, got, label):
     neon = run_oracle(path, seq, O.W8A8_NEON)
     rows = []
     for step, (g, w, f, n) in enumerate(zip(got, want, f32, neon)):
-        e_gpu, e_q, e_ref = rel_l2(g, w), rel_l2(w, f), rel_l2(n, w)
-        rows.append((step, e_gpu, e_q, e_ref, float(np.abs(g - w).max())))
-    print(f"{label}: step, rel_l2(gpu, oracle W8A8), rel_l2(W8A8, W8A32), rel_l2(neon, scalar), max|d|")
+        rows.append((step, rel_l2(g, w), rel_l2(g, f), rel_l2(w, f), rel_l2(n, w),
+                     float(np.abs(g - w).max())))
+    print(f"{label}: step, rel_l2(gpu, W8A8), rel_l2(gpu, W8A32), rel_l2(W8A8, W8A32) = gap, "
+          f"rel_l2(neon order, scalar), max|gpu - W8A8|")
     for r in rows:
-        print("   %2d  %.2e  %.2e  %.2e  %.2e" % r)
-    for step, e_gpu, e_q, e_ref, mx in rows:
-        assert e_gpu <= REL_TOL_FACTOR * e_q, f"step {step}: {e_gpu:.3e} > {REL_TOL_FACTOR} x {e_q:.3e}"
+        print("   %2d  %.2e  %.2e  %.2e  %.2e  %.2e" % r)
+    for step, e_pair, e_f32, gap, e_ref, mx in rows:
+        assert e_f32 <= F32_FACTOR * gap, f"step {step}: {e_f32:.3e} > {F32_FACTOR} x {gap:.3e}"
+        assert e_pair <= PAIR_FACTOR * gap, f"step {step}: {e_pair:.3e} > {PAIR_FACTOR} x {gap:.3e}"
     return rows
 
 
@@ -101,6 +111,7 @@ def test_teacher_forced_logits(tiny_gguf, wtype, variant):
         assert t == O.greedy(g), "device argmax disagrees with the greedy rule on its own logits"
 
 
+@pytest.mark.skip(reason=A32_SKIP)
 def test_f32_acts_ablation(tiny_gguf):
     """SQUIRREL_F32_ACTS=1 (linear.rs:14-19): W8A32 on both sides."""
     path = tiny_gguf("Q8_0", "g4")
@@ -247,10 +258,12 @@ def test_full_size_q8_0_prefill_and_decode(model_dir):
     got, toks, _ = run_gpu(path, seq, max_pos=64)
     want = run_oracle(path, seq, O.W8A8, max_pos=64)
     f32 = run_oracle(path, seq, O.W8A32, max_pos=64)
-    for step, (g, w, f) in enumerate(zip(got, want, f32)):
-        e_gpu, e_q = rel_l2(g, w), rel_l2(w, f)
-        print(f"full-size Q8_0 step {step}: rel_l2 gpu/oracle {e_gpu:.2e}, W8A8/W8A32 {e_q:.2e}, "
-              f"max|d| {float(np.abs(g - w).max()):.2e}, top1 gpu {int(np.argmax(g))} oracle {int(np.argmax(w))}")
-        assert e_gpu <= REL_TOL_FACTOR * e_q
+    neon = run_oracle(path, seq, O.W8A8_NEON, max_pos=64)
+    for step, (g, w, f, n) in enumerate(zip(got, want, f32, neon)):
+        e_pair, e_f32, gap, e_ref = rel_l2(g, w), rel_l2(g, f), rel_l2(w, f), rel_l2(n, w)
+        print(f"full-size Q8_0 step {step}: rel_l2 gpu/W8A8 {e_pair:.2e}, gpu/W8A32 {e_f32:.2e}, "
+              f"gap W8A8/W8A32 {gap:.2e}, neon/scalar {e_ref:.2e}, max|d| {float(np.abs(g - w).max()):.2e}, "
+              f"top1 gpu {int(np.argmax(g))} oracle {int(np.argmax(w))} neon {int(np.argmax(n))}")
+        assert e_f32 <= F32_FACTOR * gap and e_pair <= PAIR_FACTOR * gap
     for g, t in zip(got, toks):
         assert t == O.greedy(g)
