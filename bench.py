@@ -9,9 +9,10 @@ and is reported separately as prefill tok/s (the reference's convention:
 decode throughput excludes step 1, scripts/bench.py:68-71).  Weights are
 random-init from a fixed seed (synthetic data; no checkpoint is available).
 
-One JSON line is printed.  `roofline` prices the dominant kernel (the fused
-gate/up matvec) against MI355X's 8 TB/s HBM peak using its algorithmic bytes
-and its mean duration measured here with HIP events; `cpu_baseline` is the
+One JSON line is printed.  `roofline` prices the dominant kernel against
+MI355X's 8 TB/s HBM peak using its algorithmic bytes and its mean duration
+measured here with HIP events: the persistent decode-step kernel (one launch
+per token), or with --multi-kernel the fused gate/up matvec; `cpu_baseline` is the
 oracle (the C restatement of the reference's x86 scalar path) timed on this
 host over a bounded sample of the same workload.
 """
@@ -110,11 +111,11 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
-def measured_traffic(config: str):
+def measured_traffic(kernel: str, config: str):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by the copy calibration),
-    or None when no measurement exists for this workload."""
-    path = os.path.join(REPO, "profiles", f"traffic_gate_up_matvec_{config}.json")
+    or None when no measurement exists for this kernel and workload."""
+    path = os.path.join(REPO, "profiles", f"traffic_{kernel}_{config}.json")
     try:
         with open(path) as f:
             return int(json.load(f)["traffic_bytes_per_launch"])
@@ -133,6 +134,8 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=None,
                     help="decode steps timed on the CPU (default: the same count as the GPU run)")
     ap.add_argument("--kernel-iters", type=int, default=200)
+    ap.add_argument("--multi-kernel", action="store_true",
+                    help="decode with one kernel per op (hipGraph) instead of the persistent step kernel")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB five times (the known-size "
                          "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
@@ -156,7 +159,7 @@ def main() -> int:
     log(f"loaded {path} ({info.weight_bytes / 1e6:.1f} MB of matrices) in {time.time() - t0:.1f}s")
     S = cfg["prompt"]
     prompt = np.random.default_rng(args.seed).integers(0, info.vocab, S).astype(np.uint32)
-    ctx = model.new_context(S + max(K, W) + 2)
+    ctx = model.new_context(S + max(K, W) + 2, persistent=not args.multi_kernel)
     gen = sqhip.TextTokenGenerator(model, ctx)
 
     if W > 0:
@@ -182,11 +185,22 @@ def main() -> int:
         us, nbytes = ctx.time_kernel(which, args.kernel_iters)
         kernels[name] = {"mean_us": round(us, 3), "bytes": int(nbytes),
                          "gbs": round(nbytes / us / 1e3, 1)}
-    dom = kernels["gate_up_matvec"]
-    roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
-                "kernel": "gate_up_matvec (layer 0: RMSNorm+Q8 prologue, 16384x2048 Q8_0 "
-                          "matvec, SiLU*up+Q8 epilogue)"}
+    if ctx.persistent:
+        # The whole decode step is one kernel: its algorithmic bytes per launch
+        # over its mean duration from the HIP events around every step.
+        roofline = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic("decode_step", args.config),
+                    "kernel": "decode_step_kernel (persistent: one launch per token, all 16 layers + "
+                              "LM head + argmax)",
+                    "bytes_per_launch": int(avg_bytes)}
+    else:
+        dom = kernels["gate_up_matvec"]
+        roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic("gate_up_matvec", args.config),
+                    "kernel": "gate_up_matvec (RMSNorm+Q8 prologue, 16384x2048 Q8_0 matvec, "
+                              "SiLU*up+Q8 epilogue)"}
 
     cpu = None
     if not args.no_cpu:

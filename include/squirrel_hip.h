@@ -50,7 +50,9 @@ extern "C" {
 
 /* Context flags */
 #define SQ_CTX_F32_ACTS 1u  /* SQUIRREL_F32_ACTS=1 (src/ops/linear.rs:14-19): W8A32 matvecs */
-#define SQ_CTX_NO_GRAPH 2u  /* launch the decode step kernel by kernel (no hipGraph) */
+#define SQ_CTX_NO_GRAPH 2u  /* multi-kernel decode: launch kernel by kernel (no hipGraph) */
+#define SQ_CTX_MULTI_KERNEL 4u /* decode with one kernel per op (a hipGraph) instead of the
+                                  persistent one-launch-per-token kernel */
 
 /* Generation flags */
 #define SQ_GEN_IGNORE_EOS 1u  /* SQUIRREL_IGNORE_EOS=1 (src/text_generator.rs:15-19) */
@@ -116,6 +118,23 @@ int sq_ctx_new(const sq_model* m, size_t max_positions, uint32_t flags, sq_ctx**
 void sq_ctx_free(sq_ctx* c);
 /* ModelContext::reset_cache (context.rs:25-27). */
 int sq_ctx_reset(sq_ctx* c);
+/* How decode steps run: 1 = the persistent one-launch-per-token kernel
+ * (Q8_0 / Q4_0 integer path, head_dim 64, width <= 2048), 0 = one kernel per
+ * op replayed as a hipGraph.  No reference counterpart (measurement aid). */
+int sq_ctx_decode_kernel(const sq_ctx* c);
+/* Timeline of the persistent decode step (measurement aid, no reference
+ * counterpart).  With tracing enabled every step records, per workgroup,
+ * `stride` wall-clock stamps (device wall clock, hipDeviceAttributeWallClockRate
+ * kHz): [0] start; for layer l at [1 + 16l + j]: j = 0 QKV inputs gathered,
+ * 1 QKV done, 2 attention done, 3 tile merge done, 4 o-projection inputs
+ * gathered, 5 o-projection done, 6 gate/up inputs gathered, 7 gate/up dot
+ * done, 8 gate/up done, 9 down inputs gathered, 10 down done; then
+ * [1 + 16L] LM-head inputs gathered, [2 + 16L] LM head done, [3 + 16L] token
+ * resolved (workgroup 0 only); 0 where a slot was not reached.
+ * _read copies the most recent step's stamps (grid * stride values); with
+ * out == NULL it only reports grid and stride. */
+int sq_ctx_step_trace(sq_ctx* c, int enable);
+int sq_ctx_step_trace_read(sq_ctx* c, uint64_t* out, size_t n, int* grid, int* stride);
 size_t sq_ctx_seq_len(const sq_ctx* c);
 
 /* Model::forward (model.rs:45-97): n > 1 runs the batched prefill, n == 1 a

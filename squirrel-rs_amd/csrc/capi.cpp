@@ -153,7 +153,47 @@ int sq_ctx_reset(sq_ctx* c) {
     c->seq_len = 0;
     SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
     SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
+    if (c->persist) {
+        // Clear a raised error and move the tag epoch past every tag an
+        // abandoned step may have written (tags are never reused).
+        unsigned epoch = 0;
+        SQ_HIP_CHECK(hipMemcpy(&epoch, c->s_epoch, 4, hipMemcpyDeviceToHost));
+        epoch += 2u * (6u * (unsigned)c->m->cfg.n_layers + 2u);
+        SQ_HIP_CHECK(hipMemcpy(c->s_epoch, &epoch, 4, hipMemcpyHostToDevice));
+        SQ_HIP_CHECK(hipMemset(c->s_error, 0, 4));
+    }
     SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int sq_ctx_decode_kernel(const sq_ctx* c) { return c && c->persist ? 1 : 0; }
+
+int sq_ctx_step_trace(sq_ctx* c, int enable) {
+    if (!c) return set_error(SQ_ERR_ARG, "step_trace: null context");
+    if (!c->persist) return set_error(SQ_ERR_UNSUPPORTED, "step_trace: the context has no persistent decode step");
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (!enable) {
+        c->step.trace = nullptr;
+        return 0;
+    }
+    const int stride = 16 * c->m->cfg.n_layers + 4;
+    if (!c->s_trace) SQ_HIP_CHECK(hipMalloc((void**)&c->s_trace, (size_t)c->step_grid * stride * 8));
+    SQ_HIP_CHECK(hipMemset(c->s_trace, 0, (size_t)c->step_grid * stride * 8));
+    c->step.trace = c->s_trace;
+    c->step.trace_stride = stride;
+    return 0;
+}
+
+int sq_ctx_step_trace_read(sq_ctx* c, uint64_t* out, size_t n, int* grid, int* stride) {
+    if (!c || !grid || !stride) return set_error(SQ_ERR_ARG, "step_trace_read: null argument");
+    if (!c->s_trace || !c->step.trace) return set_error(SQ_ERR_ARG, "step_trace_read: tracing is not enabled");
+    *grid = c->step_grid;
+    *stride = c->step.trace_stride;
+    const size_t need = (size_t)c->step_grid * c->step.trace_stride;
+    if (!out) return 0;
+    if (n < need) return set_error(SQ_ERR_ARG, "step_trace_read: buffer too small");
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    SQ_HIP_CHECK(hipMemcpy(out, c->s_trace, need * 8, hipMemcpyDeviceToHost));
     return 0;
 }
 
@@ -167,6 +207,7 @@ int sq_forward(const sq_model* m, sq_ctx* c, const uint32_t* ids, size_t n) {
 int sq_logits(sq_ctx* c, float* out, size_t n) {
     if (!c || !out || n < (size_t)c->m->cfg.vocab) return set_error(SQ_ERR_ARG, "logits: buffer too small");
     SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (int st = ctx_check(c)) return st;
     SQ_HIP_CHECK(hipMemcpy(out, c->logits, (size_t)c->m->cfg.vocab * 4, hipMemcpyDeviceToHost));
     return 0;
 }
@@ -174,6 +215,7 @@ int sq_logits(sq_ctx* c, float* out, size_t n) {
 int sq_argmax(sq_ctx* c, uint32_t* token) {
     if (!c || !token) return set_error(SQ_ERR_ARG, "argmax: null argument");
     SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (int st = ctx_check(c)) return st;
     SQ_HIP_CHECK(hipMemcpy(token, c->d_token, 4, hipMemcpyDeviceToHost));
     return 0;
 }
@@ -181,6 +223,7 @@ int sq_argmax(sq_ctx* c, uint32_t* token) {
 int sq_ctx_last_hidden(sq_ctx* c, float* out, size_t n) {
     if (!c || !out || n < (size_t)c->m->cfg.dim) return set_error(SQ_ERR_ARG, "last_hidden: buffer too small");
     SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (int st = ctx_check(c)) return st;
     SQ_HIP_CHECK(hipMemcpy(out, c->last_hidden, (size_t)c->m->cfg.dim * 4, hipMemcpyDeviceToHost));
     return 0;
 }
@@ -189,6 +232,7 @@ int sq_ctx_debug_act(sq_ctx* c, float* normed, void* blocks) {
     if (!c) return set_error(SQ_ERR_ARG, "debug_act: null context");
     const size_t D = c->m->cfg.dim;
     SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (int st = ctx_check(c)) return st;
     if (normed) SQ_HIP_CHECK(hipMemcpy(normed, c->dbg_normed, D * 4, hipMemcpyDeviceToHost));
     if (blocks) {
         std::vector<int8_t> qs(D);
@@ -208,7 +252,9 @@ int sq_generate(const sq_model* m, sq_ctx* c, const uint32_t* prompt, size_t n_p
                 uint32_t flags, uint32_t* out_tokens, size_t* n_out, double* step_ms) {
     if (!m || !c || c->m != m || !n_out || (max_tokens && !out_tokens))
         return set_error(SQ_ERR_ARG, "generate: bad argument");
-    return ctx_generate(c, prompt, n_prompt, max_tokens, flags, out_tokens, n_out, step_ms);
+    int st = ctx_generate(c, prompt, n_prompt, max_tokens, flags, out_tokens, n_out, step_ms);
+    if (st) return st;
+    return ctx_check(c);
 }
 
 int sq_ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes) {

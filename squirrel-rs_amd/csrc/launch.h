@@ -122,4 +122,69 @@ int launch_copy_i32(hipStream_t s, const int* src, int* dst);
 int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq,
                 const uint16_t* ad, const float* x, int m, float* out, int ldo, bool accumulate);
 
+// ---- persistent decode step (k_step.hip) -----------------------------------
+struct StepLayer {
+    MatView qkv, o, gateup, down;
+    const float* attn_norm;
+    const float* ffn_norm;
+};
+
+// Exchange words of the persistent decode step: payload in the low 32 bits,
+// the producing phase's tag in the high 32 bits.
+struct Xchg {
+    unsigned long long* h;  // hidden row [dim]
+    unsigned long long* q;  // q after RoPE [n_heads*64]
+    unsigned long long* k;  // new K row [n_kv_heads*64]
+    unsigned long long* v;  // new V row [n_kv_heads*64]
+    unsigned long long* a;  // attention row as Q8_0: payload [q_dim/4] then scales [q_dim/32]
+    unsigned long long* f;  // FFN activation as Q8_0: payload [ffn/4] then scales [ffn/32]
+    unsigned long long* p;  // argmax partials [3 * grid]
+    unsigned long long* t;  // attention tile partials [n_heads][max_tiles][64 + 2]
+};
+size_t exchange_words(int dim, int ffn, int n_heads, int n_kv_heads, int max_tiles, int grid);
+
+// Everything one decode step reads and writes.  The launch reads *pos,
+// *token and *epoch; workgroup 0 writes the next token, appends it to
+// history[*n_hist], advances *pos and *epoch.  *epoch starts at zero and is
+// never rewound; *error is raised when a wait exceeds spin_limit wall-clock
+// ticks, after which every workgroup leaves.
+struct StepArgs {
+    const StepLayer* layers;  // device array [n_layers]
+    MatView embd, head;
+    const float* out_norm;
+    int n_layers, dim, ffn, n_heads, n_kv_heads, vocab;
+    float eps;
+    Xchg x;
+    float* kcache;
+    float* vcache;
+    size_t kv_layer;  // floats per layer of each cache
+    const float2* rope;
+    int* pos;
+    uint32_t* token;
+    uint32_t* history;
+    int* n_hist;
+    float* logits;
+    int max_tiles;
+    unsigned* epoch;
+    int* error;
+    long long spin_limit;
+    float* dbg_normed;  // layer-0 attention norm (workgroup 0), optional
+    int8_t* dbg_qs;
+    uint16_t* dbg_d;
+    float* last_hidden;  // final norm (workgroup 0), optional
+    int8_t* head_qs;
+    uint16_t* head_d;
+    // Optional timeline (measurement): per workgroup, trace_stride wall-clock
+    // stamps, 16 slots per layer (k_step.hip TraceSlot) after slot 0 (start).
+    unsigned long long* trace;
+    int trace_stride;
+};
+
+// True when the step kernel can run the model with `grid` workgroups.
+bool decode_step_fits(int dim, int ffn, int n_heads, int n_kv_heads, int grid);
+// Launch of one decode step over `grid` workgroups (one per CU).
+int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid);
+// Workgroups for the decode step on the current device (one per CU).
+int decode_step_max_grid(int wtype, int* grid);
+
 }  // namespace sq

@@ -549,6 +549,7 @@ int build_decode_step(sq_ctx* c) {
 }
 
 int run_decode_step(sq_ctx* c) {
+    if (c->persist) return launch_decode_step(c->stream, c->m->wtype, c->step, c->step_grid);
     if (c->graph) {
         SQ_HIP_CHECK(hipGraphLaunch(c->graph, c->stream));
         return 0;
@@ -627,6 +628,92 @@ int run_prefill(sq_ctx* c, size_t n) {
 
 }  // namespace
 
+// The persistent decode step serves integer-path Q8_0 / Q4_0 models with
+// head_dim 64 (the multi-kernel hipGraph path serves the rest, and any context
+// created with SQ_CTX_MULTI_KERNEL).
+int setup_persistent(sq_ctx* c) {
+    const sq_model* m = c->m;
+    const Config& g = m->cfg;
+    if ((c->flags & SQ_CTX_MULTI_KERNEL) || !c->a8 || (m->wtype != WT_Q8_0 && m->wtype != WT_Q4_0) ||
+        g.head_dim != 64)
+        return 0;
+    int grid = 0, st;
+    if ((st = decode_step_max_grid(m->wtype, &grid))) return st;
+    if (!decode_step_fits(g.dim, g.ffn, g.n_heads, g.n_kv_heads, grid)) return 0;
+    const int QD = g.n_heads * g.head_dim, KVD = g.n_kv_heads * g.head_dim;
+    std::vector<StepLayer> hl(g.n_layers);
+    for (int l = 0; l < g.n_layers; l++) {
+        const Layer& L = m->layers[l];
+        hl[l] = StepLayer{view(L.qkv), view(L.o), view(L.gateup), view(L.down), L.attn_norm, L.ffn_norm};
+    }
+    const size_t nx = exchange_words(g.dim, g.ffn, g.n_heads, g.n_kv_heads, c->max_tiles, grid);
+    if ((st = dmalloc(&c->d_layers, (size_t)g.n_layers)) || (st = dmalloc(&c->s_xchg, nx)) ||
+        (st = dmalloc(&c->s_epoch, 1)) || (st = dmalloc(&c->s_error, 1)))
+        return st;
+    SQ_HIP_CHECK(hipMemcpy(c->d_layers, hl.data(), hl.size() * sizeof(StepLayer), hipMemcpyHostToDevice));
+    SQ_HIP_CHECK(hipMemset(c->s_xchg, 0, nx * 8));
+    SQ_HIP_CHECK(hipMemset(c->s_epoch, 0, 4));
+    SQ_HIP_CHECK(hipMemset(c->s_error, 0, 4));
+    int dev = 0, khz = 0;
+    SQ_HIP_CHECK(hipGetDevice(&dev));
+    SQ_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    StepArgs& a = c->step;
+    a.layers = c->d_layers;
+    a.embd = view(m->embd);
+    a.head = view(m->head);
+    a.out_norm = m->out_norm;
+    a.n_layers = g.n_layers;
+    a.dim = g.dim;
+    a.ffn = g.ffn;
+    a.n_heads = g.n_heads;
+    a.n_kv_heads = g.n_kv_heads;
+    a.vocab = g.vocab;
+    a.eps = g.eps;
+    unsigned long long* x = c->s_xchg;
+    a.x.h = x; x += g.dim;
+    a.x.q = x; x += QD;
+    a.x.k = x; x += KVD;
+    a.x.v = x; x += KVD;
+    a.x.a = x; x += QD / 4 + QD / 32;
+    a.x.f = x; x += g.ffn / 4 + g.ffn / 32;
+    a.x.p = x; x += 3 * (size_t)grid;
+    a.x.t = x;
+    a.kcache = c->kcache;
+    a.vcache = c->vcache;
+    a.kv_layer = c->max_pos * (size_t)KVD;
+    a.rope = c->rope;
+    a.pos = c->d_pos;
+    a.token = c->d_token;
+    a.history = c->d_hist;
+    a.n_hist = c->d_nhist;
+    a.logits = c->logits;
+    a.max_tiles = c->max_tiles;
+    a.epoch = c->s_epoch;
+    a.error = c->s_error;
+    a.spin_limit = (long long)khz * 250;  // 250 ms
+    a.dbg_normed = c->dbg_normed;
+    a.dbg_qs = c->dbg_qs;
+    a.dbg_d = c->dbg_d;
+    a.last_hidden = c->last_hidden;
+    a.head_qs = c->head_qs;
+    a.head_d = c->head_d;
+    a.trace = nullptr;
+    a.trace_stride = 0;
+    c->step_grid = grid;
+    c->persist = true;
+    return 0;
+}
+
+int ctx_check(sq_ctx* c) {
+    if (!c->persist) return 0;
+    int err = 0;
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    SQ_HIP_CHECK(hipMemcpy(&err, c->s_error, 4, hipMemcpyDeviceToHost));
+    if (err)
+        return set_error(SQ_ERR_HIP, "decode step: a grid barrier wait timed out; the context must be reset");
+    return 0;
+}
+
 int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) {
     if (!m || max_pos == 0) return set_error(SQ_ERR_ARG, "ctx_new: null model or zero positions");
     if (flags & SQ_CTX_F32_ACTS) return set_error(SQ_ERR_UNSUPPORTED, kA32Disabled);
@@ -701,6 +788,7 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
         ce = hipGraphInstantiate(&c->graph, gr, nullptr, nullptr, 0);
         if (ce != hipSuccess) return fail(set_error(SQ_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ce)));
     }
+    if ((st = setup_persistent(c))) return fail(st);
     SQ_HIP_CHECK(hipDeviceSynchronize());
     *out = c;
     return 0;
@@ -718,6 +806,7 @@ void ctx_destroy(sq_ctx* c) {
     dfree(c->dbg_qs); dfree(c->dbg_d); dfree(c->last_hidden); dfree(c->head_qs); dfree(c->head_d);
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
     dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad);
+    dfree(c->d_layers); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
     if (c->h_pinned) (void)hipHostFree(c->h_pinned);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;

@@ -109,6 +109,16 @@ struct sq_ctx {
     int8_t* p_aq = nullptr;
     uint16_t* p_ad = nullptr;
 
+    // persistent decode step (one launch per token)
+    bool persist = false;
+    int step_grid = 0;
+    sq::StepArgs step{};
+    sq::StepLayer* d_layers = nullptr;
+    unsigned long long* s_xchg = nullptr;  // exchange words
+    unsigned* s_epoch = nullptr;
+    int* s_error = nullptr;
+    unsigned long long* s_trace = nullptr;  // step timeline when enabled
+
     uint32_t* h_pinned = nullptr;  // pinned staging for ids / tokens
     hipGraphExec_t graph = nullptr;
     hipGraph_t graph_def = nullptr;
@@ -125,6 +135,8 @@ int ctx_forward(sq_ctx* c, const uint32_t* ids, size_t n);
 int ctx_generate(sq_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t max_tokens, uint32_t flags,
                  uint32_t* out, size_t* n_out, double* step_ms);
 int ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes);
+// Status of the persistent decode step's error word (synchronizes the stream).
+int ctx_check(sq_ctx* c);
 int model_load(const char* path, sq_model** out);
 // Parse + config + tensor checks only (no device allocation).
 int model_inspect(const char* path, sq_model** out);

@@ -15,7 +15,7 @@ SQ_ERR_SHAPE, SQ_ERR_INVALID_TYPE, SQ_ERR_EMPTY, SQ_ERR_ALIGN = 1, 2, 3, 4
 SQ_ERR_IO, SQ_ERR_FORMAT, SQ_ERR_CONFIG, SQ_ERR_WEIGHTS = 16, 17, 18, 19
 SQ_ERR_UNSUPPORTED, SQ_ERR_CACHE_FULL, SQ_ERR_ARG, SQ_ERR_HIP = 20, 21, 22, 64
 SQ_F32, SQ_Q4_0, SQ_Q8_0, SQ_BF16 = 0, 2, 8, 30
-SQ_CTX_F32_ACTS, SQ_CTX_NO_GRAPH = 1, 2
+SQ_CTX_F32_ACTS, SQ_CTX_NO_GRAPH, SQ_CTX_MULTI_KERNEL = 1, 2, 4
 SQ_GEN_IGNORE_EOS, SQ_GEN_NO_KV_CACHE = 1, 2
 
 
@@ -56,6 +56,9 @@ PROTOS = {
     "sq_ctx_free": ([vp], None),
     "sq_ctx_reset": ([vp], i32),
     "sq_ctx_seq_len": ([vp], sz),
+    "sq_ctx_decode_kernel": ([vp], i32),
+    "sq_ctx_step_trace": ([vp, i32], i32),
+    "sq_ctx_step_trace_read": ([vp, vp, sz, C.POINTER(i32), C.POINTER(i32)], i32),
     "sq_forward": ([vp, vp, vp, sz], i32),
     "sq_logits": ([vp, vp, sz], i32),
     "sq_argmax": ([vp, C.POINTER(u32)], i32),

@@ -9,7 +9,7 @@ import os
 
 import numpy as np
 
-from ._lib import (SQ_CTX_F32_ACTS, SQ_CTX_NO_GRAPH, SQ_GEN_IGNORE_EOS, SQ_GEN_NO_KV_CACHE,
+from ._lib import (SQ_CTX_F32_ACTS, SQ_CTX_MULTI_KERNEL, SQ_CTX_NO_GRAPH, SQ_GEN_IGNORE_EOS, SQ_GEN_NO_KV_CACHE,
                    ModelInfo, SynthSpec, check, lib)
 from .ops import BLOCK_Q8_0
 
@@ -71,8 +71,9 @@ class Llama3_2:
         return out
 
     def new_context(self, max_positions: int = 4096, f32_acts: bool = False,
-                    graph: bool = True) -> "ModelContext":
-        return ModelContext(self, max_positions, f32_acts, graph)
+                    graph: bool = True, persistent: bool = True) -> "ModelContext":
+        """persistent=False selects the one-kernel-per-op decode step."""
+        return ModelContext(self, max_positions, f32_acts, graph, persistent)
 
     def forward(self, token_ids, ctx: "ModelContext") -> None:
         ctx.forward(token_ids)
@@ -98,9 +99,11 @@ class Llama3_2:
 class ModelContext:
     """KV cache + workspace on the device (src/models/common/context.rs)."""
 
-    def __init__(self, model: Llama3_2, max_positions: int, f32_acts: bool, graph: bool):
+    def __init__(self, model: Llama3_2, max_positions: int, f32_acts: bool, graph: bool,
+                 persistent: bool = True):
         self.model = model
-        flags = (SQ_CTX_F32_ACTS if f32_acts else 0) | (0 if graph else SQ_CTX_NO_GRAPH)
+        flags = ((SQ_CTX_F32_ACTS if f32_acts else 0) | (0 if graph else SQ_CTX_NO_GRAPH)
+                 | (0 if persistent else SQ_CTX_MULTI_KERNEL))
         h = C.c_void_p()
         check(lib().sq_ctx_new(model.h, max_positions, flags, C.byref(h)))
         self.h = h.value
@@ -136,6 +139,23 @@ class ModelContext:
 
     def seq_len(self) -> int:
         return lib().sq_ctx_seq_len(self.h)
+
+    def step_trace(self, enable: bool = True) -> None:
+        """Record a per-workgroup timeline of each persistent decode step."""
+        check(lib().sq_ctx_step_trace(self.h, 1 if enable else 0))
+
+    def step_trace_read(self) -> np.ndarray:
+        """[workgroups, stamps] wall-clock ticks of the most recent step."""
+        g, st = C.c_int(), C.c_int()
+        check(lib().sq_ctx_step_trace_read(self.h, None, 0, C.byref(g), C.byref(st)))
+        out = np.zeros((g.value, st.value), np.uint64)
+        check(lib().sq_ctx_step_trace_read(self.h, out.ctypes.data, out.size, C.byref(g), C.byref(st)))
+        return out
+
+    @property
+    def persistent(self) -> bool:
+        """True when decode steps run as one persistent kernel per token."""
+        return lib().sq_ctx_decode_kernel(self.h) == 1
 
     def time_kernel(self, which: int, iters: int) -> tuple[float, int]:
         us = C.c_double()

@@ -55,9 +55,9 @@ def run_oracle(path, seq, mode, max_pos=256):
     return outs
 
 
-def run_gpu(path, seq, f32_acts=False, graph=True, max_pos=256):
+def run_gpu(path, seq, f32_acts=False, graph=True, max_pos=256, persistent=True):
     m = sq.Llama3_2(path)
-    c = m.new_context(max_pos, f32_acts=f32_acts, graph=graph)
+    c = m.new_context(max_pos, f32_acts=f32_acts, graph=graph, persistent=persistent)
     outs, toks = [], []
     c.forward(seq[0])
     outs.append(c.logits())
@@ -97,16 +97,18 @@ def check_logits(path, seq, got, label):
     return rows
 
 
+@pytest.mark.parametrize("decode", ["persistent", "multi_kernel"])
 @pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0", "BF16"])
 @pytest.mark.parametrize("variant", ["g4", "g2"])
-def test_teacher_forced_logits(tiny_gguf, wtype, variant):
+def test_teacher_forced_logits(tiny_gguf, wtype, variant, decode):
     if wtype == "BF16":
         pytest.skip(A32_SKIP)
     path = tiny_gguf(wtype, variant)
     cfg = O.OracleModel(path).cfg
     seq = teacher_seq(cfg.vocab)
-    got, toks, _ = run_gpu(path, seq)
-    check_logits(path, seq, got, f"{wtype}/{variant}")
+    got, toks, (m, c) = run_gpu(path, seq, persistent=decode == "persistent")
+    assert c.persistent == (decode == "persistent")
+    check_logits(path, seq, got, f"{wtype}/{variant}/{decode}")
     for g, t in zip(got, toks):
         assert t == O.greedy(g), "device argmax disagrees with the greedy rule on its own logits"
 
@@ -143,13 +145,74 @@ def test_fused_norm_quantize_bit_exact(tiny_gguf):
 
 
 def test_graph_matches_eager(tiny_gguf):
+    """The multi-kernel decode step replayed as a hipGraph == launched eagerly."""
     path = tiny_gguf("Q8_0", "g4")
     seq = teacher_seq(2048, seed=5)
-    a, ta, _ = run_gpu(path, seq, graph=True)
-    b, tb, _ = run_gpu(path, seq, graph=False)
+    a, ta, _ = run_gpu(path, seq, graph=True, persistent=False)
+    b, tb, _ = run_gpu(path, seq, graph=False, persistent=False)
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
     assert ta == tb
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+def test_persistent_step_across_attention_tiles(tiny_gguf, wtype):
+    """Decode positions 60..140 cross the 64-position attention tiles, which
+    adds the persistent kernel's tile-merge phase (and its extra barrier)."""
+    path = tiny_gguf(wtype, "g4")
+    seq = teacher_seq(2048, n_prompt=60, n_decode=80, seed=11)
+    got, toks, (m, c) = run_gpu(path, seq, max_pos=160)
+    assert c.persistent
+    rows = check_logits(path, seq, got, f"{wtype}/tiles")
+    assert len(rows) == 81
+    for g, t in zip(got, toks):
+        assert t == O.greedy(g)
+
+
+def test_persistent_deterministic_across_resets(tiny_gguf):
+    """Back-to-back generations, with and without a reset in between, give
+    the same tokens and logits (barrier epochs carry over between launches)."""
+    path = tiny_gguf("Q8_0", "g2")
+    m = sq.Llama3_2(path)
+    c = m.new_context(96)
+    assert c.persistent
+    gen = sq.TextTokenGenerator(m, c)
+    prompt = np.arange(1, 9, dtype=np.uint32)
+    t1, _ = gen.generate(prompt, 40, ignore_eos=True)
+    l1 = c.logits()
+    t2, _ = gen.generate(prompt, 40, ignore_eos=True)
+    l2 = c.logits()
+    c.reset_cache()
+    t3, _ = gen.generate(prompt, 40, ignore_eos=True)
+    l3 = c.logits()
+    assert list(t1) == list(t2) == list(t3)
+    assert np.array_equal(l1, l2) and np.array_equal(l1, l3)
+
+
+def test_persistent_matches_multi_kernel_generation(tiny_gguf):
+    """Greedy generations of the two decode paths agree token for token
+    until a step whose top-2 margin is within rounding noise."""
+    path = tiny_gguf("Q8_0", "g4")
+    m = sq.Llama3_2(path)
+    prompt = np.arange(3, 15, dtype=np.uint32)
+    outs = []
+    for persistent in (True, False):
+        c = m.new_context(64, persistent=persistent)
+        toks, _ = sq.TextTokenGenerator(m, c).generate(prompt, 24, ignore_eos=True)
+        outs.append(list(toks))
+    a, b = outs
+    n = next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), len(a))
+    print(f"persistent vs multi-kernel: first divergence at step {n} of {len(a)}")
+    if n < len(a):
+        # replay the common prefix through the oracle and check the margin
+        om = O.OracleModel(path)
+        oc = om.new_context(64, O.W8A8)
+        oc.forward(prompt)
+        for t in a[:n]:
+            oc.forward([t])
+        lg = np.sort(oc.logits())
+        print(f"top-2 margin at the divergence: {lg[-1] - lg[-2]:.3e}")
+        assert lg[-1] - lg[-2] < 5e-2 * max(1.0, abs(lg[-1]))
 
 
 @pytest.mark.parametrize("wtype", ["Q8_0", "BF16"])
