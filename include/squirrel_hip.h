@@ -125,12 +125,16 @@ int sq_ctx_decode_kernel(const sq_ctx* c);
 /* Timeline of the persistent decode step (measurement aid, no reference
  * counterpart).  With tracing enabled every step records, per workgroup,
  * `stride` wall-clock stamps (device wall clock, hipDeviceAttributeWallClockRate
- * kHz): [0] start; for layer l at [1 + 16l + j]: j = 0 QKV inputs gathered,
- * 1 QKV done, 2 attention done, 3 tile merge done, 4 o-projection inputs
- * gathered, 5 o-projection done, 6 gate/up inputs gathered, 7 gate/up dot
- * done, 8 gate/up done, 9 down inputs gathered, 10 down done; then
- * [1 + 16L] LM-head inputs gathered, [2 + 16L] LM head done, [3 + 16L] token
- * resolved (workgroup 0 only); 0 where a slot was not reached.
+ * kHz): [0] start; for layer l at [1 + 20l + j]: j = 0 QKV input row gathered
+ * and quantized, 1 QKV done, 2 attention done, 3 tile merge done, 4 o-projection
+ * inputs gathered, 5 o-projection done, 6 gate/up input row gathered and
+ * quantized, 7 gate/up dot done, 8 gate/up done, 9 down inputs gathered,
+ * 10 down done, 11-13 the first attention item's q gathered / scores /
+ * outputs published, 14-15 durations (ticks) the first compute wavefront
+ * waited for weights in the gate/up phase / the layer, 16-17 the activation
+ * read back after slots 0 / 6; then [1 + 20L] LM-head inputs gathered,
+ * [2 + 20L] LM head done, [3 + 20L] token resolved (workgroup 0 only); 0 where
+ * a slot was not reached.
  * _read copies the most recent step's stamps (grid * stride values); with
  * out == NULL it only reports grid and stride. */
 int sq_ctx_step_trace(sq_ctx* c, int enable);

@@ -176,7 +176,7 @@ int sq_ctx_step_trace(sq_ctx* c, int enable) {
         c->step.trace = nullptr;
         return 0;
     }
-    const int stride = 16 * c->m->cfg.n_layers + 4;
+    const int stride = 20 * c->m->cfg.n_layers + 4;
     if (!c->s_trace) SQ_HIP_CHECK(hipMalloc((void**)&c->s_trace, (size_t)c->step_grid * stride * 8));
     SQ_HIP_CHECK(hipMemset(c->s_trace, 0, (size_t)c->step_grid * stride * 8));
     c->step.trace = c->s_trace;

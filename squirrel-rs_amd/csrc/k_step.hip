@@ -1,62 +1,126 @@
 // Persistent decode step: one launch computes a whole token.
 //
 // The decode step is a chain of dependent matvecs (per layer: QKV, attention,
-// o-projection, gate/up, down; then the LM head).  As separate kernels every
-// link pays a launch, a ramp-up and a tail.  Here one workgroup per CU stays
-// resident for the whole token and the links are data dependencies between
-// workgroups, resolved through memory:
+// o-projection, gate/up, down; then the LM head).  One workgroup per CU stays
+// resident for the whole token; the chain's links are data dependencies
+// between workgroups, resolved through memory.
 //
-// * Exchange words.  Every value handed from one phase to the next (hidden
-//   row, q row, the new K/V row, quantized activations, argmax partials) is
-//   stored as a 64-bit word: payload in the low half, the producing phase's
-//   tag in the high half, with an agent-scope atomic store (coherent across
-//   the XCDs' L2s, single-copy atomic).  A consumer polls the words it needs
-//   with agent-scope loads until each carries the expected tag.  There are no
-//   grid barriers, no flags and no store-completion waits: a consumer starts
-//   as soon as its own inputs exist.
-// * Tags are `epoch + phase` and grow across launches (the epoch word is
-//   advanced by every launch), so a word from an earlier phase or launch never
-//   matches.  A workgroup reads a phase's inputs only when it has work in that
-//   phase; the dependency chain then guarantees no input is overwritten before
-//   every workgroup that needs it has read it.
-// * The residual stream stays in registers: wavefront w owns hidden row w and
-//   adds the o-projection and down outputs of that row to it.
-// * Weights of the next phase are requested as soon as the current phase's
-//   inputs have arrived, so the HBM stream runs ahead of the dependency chain.
-// * Every wait is bounded by a wall-clock limit and a poll count: on expiry
-//   the workgroup raises the launch's error word; every waiting workgroup sees
-//   it and leaves, so the grid always drains.
+// Weight stream.  At context set-up every weight row is copied, once, into a
+// per-CU stream: CU `wg` finds the rows it will multiply, in the order it
+// will multiply them (per layer: QKV rows, o rows, gate/up rows, down rows;
+// then its LM-head rows), as one contiguous range of HBM.  A row of k
+// elements is its block payloads (k bytes Q8_0, k/2 bytes Q4_0) followed by
+// its fp16 block scales (k/16 bytes), counted in 16-byte units.
+//
+// Roles inside a workgroup (6 wavefronts):
+// * Two loader wavefronts copy the CU's stream into a 96 KB LDS ring with
+//   direct global->LDS loads (global_load_lds_dwordx4: 1 KB per instruction,
+//   no registers held), as far ahead of the computation as the ring allows.
+//   The HBM stream so runs continuously, independent of the dependency chain.
+// * Four compute wavefronts never load weights from HBM.  A wavefront's loads
+//   complete in issue order, so a poll queued behind a weight load would wait
+//   for it; keeping the weights off the compute wavefronts keeps every poll
+//   short.  They poll the phase inputs, normalize/quantize, read their rows
+//   from the ring and publish the outputs.
+// The groups synchronize through LDS counters (units filled by the loaders,
+// units consumed by each compute wavefront); the compute group synchronizes
+// among itself through an LDS arrival counter, so no loader ever waits on a
+// workgroup barrier.
+//
+// Exchange words.  Every value handed from one phase to the next (hidden
+// row, q row, the new K/V row, quantized activations, argmax partials) is a
+// 64-bit word: payload in the low half, the producing phase's tag in the high
+// half, written with an agent-scope atomic store (coherent across the XCDs'
+// L2s, single-copy atomic).  A consumer polls the words it needs with
+// agent-scope loads until each carries the expected tag.  Tags are
+// `epoch + phase` and grow across launches (the epoch word advances with every
+// launch), so a word from an earlier phase or launch never matches.  A
+// workgroup reads a phase's inputs only when it has work in that phase; the
+// dependency chain then guarantees no input is overwritten before every
+// workgroup that needs it has read it.  The residual stream stays in
+// registers: the compute wavefront that owns a hidden row adds the o and down
+// outputs of that row to it.
+//
+// Every wait is bounded by a wall-clock limit and a poll count: on expiry the
+// workgroup raises the launch's error word; every waiting wavefront sees it
+// (or its workgroup's abort flag) and leaves, so the grid always drains.
 //
 // Arithmetic per phase is that of the multi-kernel path (k_gemv.hip,
 // k_attn.hip): the reference's integer block dot (dot_prod.rs:378-403), its
 // RMSNorm (rms_norm.rs:40-56), Q8_0 activation quantizer (dot_prod.rs:21-31),
 // interleaved RoPE (rope.rs:7-36), SDPA (attention.rs:11-70), SiLU
 // (silu.rs, sigmoid.rs) and greedy tie rule (greedy.rs:6-15).
+#include <type_traits>
+
 #include "launch.h"
 
 namespace sq {
 
 namespace {
 
-constexpr int SW = 8;          // wavefronts per workgroup
-constexpr int SNT = SW * 64;   // threads per workgroup
-constexpr int HDIM = 64;       // head_dim
-constexpr int TPOS = 64;       // attention positions per tile
-constexpr int CHUNK = 1;       // tiles per attention work item
-constexpr int DMAX = 2048;     // model width supported
-constexpr int FMAX = 8192;     // FFN width supported
-constexpr int MAXG = 8;        // GQA group size supported
+constexpr int NCW = 4;             // compute wavefronts
+constexpr int NLW = 2;             // loader wavefronts
+constexpr int SW = NCW + NLW;      // wavefronts per workgroup
+constexpr int SNT = SW * 64;       // threads per workgroup
+constexpr int CNT = NCW * 64;      // compute threads
+constexpr int RU = 9216;           // ring size in 16-byte units (144 KB), a multiple of 64
+constexpr int LBATCH = 16;         // 1 KB direct-to-LDS instructions per loader batch (two in flight)
+constexpr int HDIM = 64;           // head_dim
+constexpr int TPOS = 64;           // attention positions per tile
+constexpr int DMAX = 2048;         // model width supported (one 32-block per lane)
+constexpr int FMAX = 8192;         // FFN width supported
+constexpr int MAXG = 4;            // GQA group size supported (one compute wavefront per head)
+constexpr int RMAX = 2;            // residual rows a compute wavefront owns
 constexpr int XMAX = FMAX / 4 + FMAX / 32;  // exchange words gathered at once
-constexpr int WPT = (XMAX + SNT - 1) / SNT; // ... per thread
+constexpr int WPT = (XMAX + CNT - 1) / CNT;  // ... per compute thread
 
 typedef float sq_v4f __attribute__((ext_vector_type(4)));
 typedef unsigned long long u64;
 
-// ---- global address space ----------------------------------------------------
+// ---- the per-CU weight stream ---------------------------------------------------
+struct StreamGeo {
+    int nq, no, ng, nd, nh;    // rows per phase: QKV, o, gate/up, down, LM head
+    int ua, uo, ud;            // units per row at k = dim, q_dim, ffn
+    int offo, offg, offd, LU;  // unit offsets of o, gate/up, down in a layer; units per layer
+    int total;                 // units in this CU's stream
+    int row0q, row0o, row0h;   // first row of this CU in QKV, o/down, LM head
+    int tile;                  // gate/up tile: gate rows tile*32.., up rows ffn + tile*32..
+};
+
+__host__ __device__ inline int stream_row_units(int wt, int k) { return (wt == WT_Q8_0 ? k / 16 : k / 32) + k / 256; }
+
+// QKV: nq consecutive rows of the stacked q|k|v matrix (whole RoPE pairs).
+// o and down: the same no rows (the hidden rows this CU owns).  Gate/up: the
+// 32 gate and 32 up rows of one 32-wide FFN tile (CUs below ffn/32).  Head:
+// nh consecutive vocabulary rows.  Rows past a matrix's end repeat row 0.
+__host__ __device__ inline StreamGeo stream_geo(int wt, int L, int D, int F, int QD, int KVD, int vocab, int G,
+                                                int wg) {
+    StreamGeo g;
+    const int q_units = (QD + 2 * KVD) / 2;
+    g.nq = 2 * ((q_units + G - 1) / G);
+    g.no = (D + G - 1) / G;
+    g.ng = wg < F / 32 ? 64 : 0;
+    g.nd = g.no;
+    g.nh = (vocab + G - 1) / G;
+    g.ua = stream_row_units(wt, D);
+    g.uo = stream_row_units(wt, QD);
+    g.ud = stream_row_units(wt, F);
+    g.offo = g.nq * g.ua;
+    g.offg = g.offo + g.no * g.uo;
+    g.offd = g.offg + g.ng * g.ua;
+    g.LU = g.offd + g.nd * g.ud;
+    g.total = L * g.LU + g.nh * g.ua;
+    g.row0q = wg * g.nq;
+    g.row0o = wg * g.no;
+    g.row0h = wg * g.nh;
+    g.tile = wg;
+    return g;
+}
+
+// ---- address spaces ------------------------------------------------------------
 // Pointers read from memory (the per-layer views) are generic to the
-// compiler, which would access them with flat instructions.  A flat load also
-// counts against lgkmcnt, so every LDS or scalar wait would stall behind the
-// weight stream.  All device-memory accesses here go through these casts.
+// compiler, which would access them with flat instructions (flat loads also
+// count against lgkmcnt).  All device-memory accesses go through these casts.
 template <typename T>
 using gptr = __attribute__((address_space(1))) T*;
 template <typename T>
@@ -67,22 +131,10 @@ template <typename T>
 __device__ __forceinline__ gptr<const T> gl(const T* p) {
     return (gptr<const T>)p;
 }
-
 // Read-only for the whole launch (per-layer views): constant address space,
-// so the compiler reads it with scalar loads instead of vector loads that
-// would queue behind the weight stream.
+// read with scalar loads.
 template <typename T>
 using cptr = const __attribute__((address_space(4))) T*;
-
-__device__ __forceinline__ MatView view_of(const __attribute__((address_space(4))) MatView& v) {
-    MatView m;
-    m.qs = v.qs;
-    m.scale = v.scale;
-    m.rows = v.rows;
-    m.k = v.k;
-    m.wtype = v.wtype;
-    return m;
-}
 
 template <typename T>
 __device__ __forceinline__ T ld_c(const T* p) {
@@ -97,23 +149,107 @@ __device__ __forceinline__ void put(u64* p, unsigned payload, unsigned tag) {
 }
 __device__ __forceinline__ void putf(u64* p, float v, unsigned tag) { put(p, __builtin_bit_cast(unsigned, v), tag); }
 
-// ---- waiting ---------------------------------------------------------------
+// ---- wavefront sum without LDS ------------------------------------------------
+// DPP butterfly: quad swaps, half-row and row mirrors leave every lane of a
+// 16-lane row with the row's sum; two row broadcasts accumulate the rows into
+// lane 63, which is read back as a wave-uniform value.  (The shuffle-based
+// sum would go through the LDS crossbar, which the ring keeps busy.)
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float wave_total(float v) {
+    v += dpp_mov<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141, 0xF>(v);  // row_half_mirror
+    v += dpp_mov<0x140, 0xF>(v);  // row_mirror
+    v += dpp_mov<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_mov<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+// The same butterfly with fmaxf.
+__device__ __forceinline__ float wave_maximum(float v) {
+    v = fmaxf(v, dpp_mov<0xB1, 0xF>(v));
+    v = fmaxf(v, dpp_mov<0x4E, 0xF>(v));
+    v = fmaxf(v, dpp_mov<0x141, 0xF>(v));
+    v = fmaxf(v, dpp_mov<0x140, 0xF>(v));
+    const float b15 = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+    v = fmaxf(v, b15);
+    const float b31 = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+    v = fmaxf(v, b31);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float lane_value(float v, int lane_index) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane_index));
+}
+
+// ---- shared state ---------------------------------------------------------------
+struct StepShared {
+    alignas(16) uint8_t ring[RU * 16];   // weight ring (loaders write, compute reads)
+    alignas(16) unsigned xw[XMAX];       // gathered exchange payloads
+    alignas(16) int aq[DMAX / 4];        // normalized activation as Q8_0: payload (32 int8 per block)
+    float as[DMAX / 32];                 // ... block scales (f32 of the fp16 scale)
+    int asum[DMAX / 32];                 // ... sums of each block's payload (Q4_0 offset term)
+    float ssum[NCW];                     // per-wavefront partial sums of squares
+    float gu[64];                        // gate/up outputs of the workgroup's tile
+    float bv[NCW];
+    int bi[NCW];
+    int bn[NCW];
+    int done[NLW];  // per loader: its next instruction (all its earlier ones are in LDS)
+    int cons[NCW];  // per compute wavefront: stream units consumed (its entries ending at or below)
+    int csync;      // compute-group arrival counter
+    int abort;
+};
+
+template <typename T>
+__device__ __forceinline__ T lds_ld(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+template <typename T>
+__device__ __forceinline__ void lds_st(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+template <typename T>
+__device__ __forceinline__ void lds_release(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// ---- bounded waiting ------------------------------------------------------------
 struct Ctl {
     int* error;
     long long limit;  // wall-clock ticks one wait may take
 };
 
-// Poll one word until it carries `tag`.  False on timeout or a raised error.
-__device__ __forceinline__ bool await_word(const u64* p, u64& w, unsigned tag, const Ctl& C) {
-    if ((unsigned)(w >> 32) == tag) return true;
-    const long long t0 = wall_clock64();
+// Poll exchange words p[0..N) (null: no word) until each carries `tag`.
+// Every round re-requests all words still stale at once, so a round costs one
+// memory round trip however many words are pending.  False on timeout, a
+// raised error or the workgroup's abort flag.
+template <int N>
+__device__ __forceinline__ bool await_words(const u64* const (&p)[N], u64 (&w)[N], unsigned tag, const Ctl& C,
+                                            const int* abort) {
+    auto pending = [&]() {
+        bool any = false;
+#pragma unroll
+        for (int j = 0; j < N; j++) any |= p[j] != nullptr && (unsigned)(w[j] >> 32) != tag;
+        return any;
+    };
+    if (!pending()) return true;
+    // The wall clock is first read at the first periodic check: reading it
+    // is a scalar-memory access whose latency would delay the first polls.
+    long long t0 = 0;
     for (int polls = 1;; polls++) {
-        __builtin_amdgcn_s_sleep(4);
-        w = ld_c(p);
-        if ((unsigned)(w >> 32) == tag) return true;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int j = 0; j < N; j++)
+            if (p[j] != nullptr && (unsigned)(w[j] >> 32) != tag) w[j] = ld_c(p[j]);
+        if (!pending()) return true;
         if ((polls & 15) == 0) {
-            if (ld_c(C.error) != 0) return false;
-            if (wall_clock64() - t0 > C.limit || polls > (1 << 20)) {
+            if (ld_c(C.error) != 0 || lds_ld(abort)) return false;
+            const long long now = wall_clock64();
+            if (polls == 16) t0 = now;
+            if (now - t0 > C.limit || polls > (1 << 20)) {
                 st_c(C.error, 1);
                 return false;
             }
@@ -121,196 +257,441 @@ __device__ __forceinline__ bool await_word(const u64* p, u64& w, unsigned tag, c
     }
 }
 
-struct StepShared {
-    alignas(16) unsigned xw[XMAX];  // gathered exchange payloads
-    alignas(16) int8_t qs[DMAX];
-    uint16_t d[DMAX / 32];
-    int asum[DMAX / 32];
-    float red[SW];
-    float gu[64];
-    float bv[SW];
-    int bi[SW];
-    int bn[SW];
-    int abort;
-    // attention
-    float k[TPOS][HDIM + 1];
-    alignas(16) float v[TPOS][HDIM];
-    float qh[MAXG][HDIM];
-    float p[MAXG][TPOS];
-    float m[MAXG], l[MAXG];
-};
+// Spin until an LDS condition holds (bounded), then acquire.  False: abandon
+// the launch.
+template <typename F>
+__device__ __forceinline__ bool spin_lds(F&& ready, StepShared& S, const Ctl& C) {
+    bool ok = true;
+    if (!ready()) {
+        long long t0 = 0;  // read at the first periodic check (see await_words)
+        for (int polls = 1;; polls++) {
+            __builtin_amdgcn_s_sleep(1);
+            if (ready()) break;
+            if ((polls & 63) == 0) {
+                if (lds_ld(&S.abort) || ld_c(C.error) != 0) {
+                    ok = false;
+                    break;
+                }
+                const long long now = wall_clock64();
+                if (polls == 64) t0 = now;
+                if (now - t0 > C.limit || polls > (1 << 24)) {
+                    st_c(C.error, 1);
+                    ok = false;
+                    break;
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    return ok;
+}
 
-// The whole workgroup gathers words src[0..n) once they carry `tag`; their
-// payloads land in S.xw.  False: the launch is being abandoned.
-__device__ __forceinline__ bool gather(StepShared& S, const u64* src, int n, unsigned tag, const Ctl& C) {
-    const int tid = threadIdx.x;
+// Compute-group barrier (the loaders take no part).  gen counts this
+// wavefront's arrivals.
+__device__ __forceinline__ bool csync(StepShared& S, int& gen, const Ctl& C) {
+    gen++;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(&S.csync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int target = NCW * gen;
+    const bool ok = spin_lds([&] { return lds_ld(&S.csync) >= target; }, S, C);
+    if (!ok) lds_st(&S.abort, 1);
+    return ok && !lds_ld(&S.abort);
+}
+
+// The compute group gathers words src[0..n) once they carry `tag`; payloads
+// land in xw.  False: abandon.
+__device__ __forceinline__ bool gather(StepShared& S, unsigned* xw, const u64* src, int n, unsigned tag, const Ctl& C,
+                                       int& gen) {
+    // t is made opaque here so that the addresses below are formed in place:
+    // hoisted out of the layer loop they would stay live (and spill)
+    int t = threadIdx.x;  // < CNT
+    asm volatile("" : "+v"(t));
+    const u64* p[WPT];
     u64 w[WPT];
 #pragma unroll
     for (int j = 0; j < WPT; j++) {
-        const int i = tid + j * SNT;
+        const int i = t + j * CNT;
+        p[j] = i < n ? src + i : nullptr;
         w[j] = i < n ? ld_c(src + i) : 0;
     }
-    bool ok = true;
+    if (!await_words(p, w, tag, C, &S.abort)) lds_st(&S.abort, 1);
 #pragma unroll
     for (int j = 0; j < WPT; j++) {
-        const int i = tid + j * SNT;
-        if (i < n && ok) {
-            ok = await_word(src + i, w[j], tag, C);
-            S.xw[i] = (unsigned)w[j];
-        }
+        const int i = t + j * CNT;
+        if (i < n) xw[i] = (unsigned)w[j];
     }
-    if (!ok) S.abort = 1;
-    __syncthreads();
-    return S.abort == 0;
+    return csync(S, gen, C);
 }
 
-// ---- weight rows held in registers ------------------------------------------
+// ---- reading rows from the ring ----------------------------------------------------
+// Ring position of the unit k units past ring position rb (rb < RU, k < RU):
+// one subtraction and an unsigned min wrap it.
+__device__ __forceinline__ unsigned ring_wrap(unsigned o) { return min(o, o - (unsigned)RU); }
+
+// Q8_0 activation block of one lane: payload q[8] (32 int8), scale s, and the
+// sum of the payload (Q4_0 offset term).
+struct ActQ {
+    int q[8];
+    float s;
+    int sum;
+};
+
+// One lane's block of one row, as read from the ring: payload (two 16-byte
+// units Q8_0, one Q4_0) and the fp16 scale.
+struct RowData {
+    uint4 w0, w1;
+    uint16_t d;
+};
+
+// Reads block `blk` of the row whose first unit sits at ring position rb (P
+// payload units).  Reads only: the batch's reads are all issued before any of
+// its arithmetic.
 template <int WT>
-struct Blk;
-template <>
-struct Blk<WT_Q8_0> { static constexpr int DW = 8; };
-template <>
-struct Blk<WT_Q4_0> { static constexpr int DW = 4; };
-
-template <int WT, int NBL, int R>
-struct Rows {
-    int w[R][NBL][Blk<WT>::DW];
-    uint16_t d[R][NBL];
-};
-
-// A zero fp16 scale: rows and blocks a lane does not own read it, so their
-// terms vanish without a branch around the loads.
-__device__ const uint16_t kZeroScale = 0;
-
-// Rows `row[r]` (negative: none) of m, the lane's blocks lane, lane+64, ...
-// Branch-free: every lane issues all its loads back to back (a missing row or
-// block reads row 0 / block 0 with a zero scale).  A branch per row would let
-// the compiler place each row's scale conversion inside the branch, making
-// every row wait for the previous row's scale load.
-template <int WT, int NBL, int R>
-__device__ __forceinline__ void load_rows(Rows<WT, NBL, R>& B, const MatView& m, const int (&row)[R], int lane) {
-    constexpr int DW = Blk<WT>::DW;
-    const int KB = m.k >> 5;
-    const size_t row_bytes = (size_t)KB * (DW * 4);
-    const gptr<const uint8_t> base = gl((const uint8_t*)m.qs);
-    const gptr<const uint16_t> scale = gl(m.scale);
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-#pragma unroll
-        for (int b = 0; b < NBL; b++) {
-            const int blk = lane + 64 * b;
-            const bool valid = row[r] >= 0 && blk < KB;
-            const size_t rr = valid ? (size_t)row[r] : 0;
-            const int bb = valid ? blk : 0;
-            const gptr<const sq_v4i> p = (gptr<const sq_v4i>)(base + rr * row_bytes + (size_t)bb * (DW * 4));
-#pragma unroll
-            for (int v = 0; v < DW / 4; v++) {
-                const sq_v4i x = __builtin_nontemporal_load(p + v);
-                B.w[r][b][4 * v + 0] = x.x;
-                B.w[r][b][4 * v + 1] = x.y;
-                B.w[r][b][4 * v + 2] = x.z;
-                B.w[r][b][4 * v + 3] = x.w;
-            }
-            B.d[r][b] = *(valid ? scale + rr * KB + bb : gl(&kZeroScale));
-        }
+__device__ __forceinline__ RowData row_fetch(const StepShared& S, unsigned rb, int P, int blk) {
+    RowData r;
+    if constexpr (WT == WT_Q8_0) {
+        r.w0 = *(const uint4*)(S.ring + ring_wrap(rb + 2 * blk) * 16);
+        r.w1 = *(const uint4*)(S.ring + ring_wrap(rb + 2 * blk + 1) * 16);
+    } else {
+        r.w0 = *(const uint4*)(S.ring + ring_wrap(rb + blk) * 16);
+        r.w1 = r.w0;
     }
+    r.d = *(const uint16_t*)(S.ring + ring_wrap(rb + P + (blk >> 3)) * 16 + (blk & 7) * 2);
+    return r;
 }
 
-// Quantized activation blocks of one lane (lane, lane+64, ...).
-template <int NBL>
-struct Act {
-    int q[NBL][8];
-    float s[NBL];
-    int sum[NBL];  // sum of the block's q (Q4_0 offset term)
-};
+// The block's term (f32(isum) * sa) * sw (dot_prod.rs:378-403); zero where
+// `valid` is false (a lane past the row's blocks reads unrelated ring bytes).
+template <int WT>
+__device__ __forceinline__ float row_math(const RowData& r, const ActQ& A, bool valid) {
+    int isum = 0;
+    if constexpr (WT == WT_Q8_0) {
+        isum = __builtin_amdgcn_sdot4(A.q[0], (int)r.w0.x, isum, false);
+        isum = __builtin_amdgcn_sdot4(A.q[1], (int)r.w0.y, isum, false);
+        isum = __builtin_amdgcn_sdot4(A.q[2], (int)r.w0.z, isum, false);
+        isum = __builtin_amdgcn_sdot4(A.q[3], (int)r.w0.w, isum, false);
+        isum = __builtin_amdgcn_sdot4(A.q[4], (int)r.w1.x, isum, false);
+        isum = __builtin_amdgcn_sdot4(A.q[5], (int)r.w1.y, isum, false);
+        isum = __builtin_amdgcn_sdot4(A.q[6], (int)r.w1.z, isum, false);
+        isum = __builtin_amdgcn_sdot4(A.q[7], (int)r.w1.w, isum, false);
+    } else {
+        const int dw[4] = {(int)r.w0.x, (int)r.w0.y, (int)r.w0.z, (int)r.w0.w};
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            isum = __builtin_amdgcn_sdot4(A.q[v], dw[v] & 0x0F0F0F0F, isum, false);
+            isum = __builtin_amdgcn_sdot4(A.q[4 + v], (dw[v] >> 4) & 0x0F0F0F0F, isum, false);
+        }
+        isum -= 8 * A.sum;
+    }
+    const float t = sq_q_term(isum, A.s, sq_f16_to_f32(r.d));
+    return valid ? t : 0.0f;
+}
 
-// res[r] = sum over blocks of (f32(isum) * sa) * sw, wavefront-reduced.
-template <int WT, int NBL, int R>
-__device__ __forceinline__ void dot_rows(const Rows<WT, NBL, R>& B, const Act<NBL>& A, int KB, int lane,
-                                         float (&res)[R]) {
+// wave_total of R values, stage by stage, so the DPP latencies overlap.
+template <int R>
+__device__ __forceinline__ void wave_totals(float (&v)[R]) {
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        float acc = 0.0f;
+    for (int r = 0; r < R; r++) v[r] += dpp_mov<0xB1, 0xF>(v[r]);
 #pragma unroll
-        for (int b = 0; b < NBL; b++) {
-            const int blk = lane + 64 * b;
-            if (blk >= KB) continue;
-            int isum = 0;
-            if constexpr (WT == WT_Q8_0) {
+    for (int r = 0; r < R; r++) v[r] += dpp_mov<0x4E, 0xF>(v[r]);
 #pragma unroll
-                for (int v = 0; v < 8; v++) isum = __builtin_amdgcn_sdot4(A.q[b][v], B.w[r][b][v], isum, false);
-            } else {
+    for (int r = 0; r < R; r++) v[r] += dpp_mov<0x141, 0xF>(v[r]);
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int dw = B.w[r][b][v];
-                    isum = __builtin_amdgcn_sdot4(A.q[b][v], dw & 0x0F0F0F0F, isum, false);
-                    isum = __builtin_amdgcn_sdot4(A.q[b][4 + v], (dw >> 4) & 0x0F0F0F0F, isum, false);
+    for (int r = 0; r < R; r++) v[r] += dpp_mov<0x140, 0xF>(v[r]);
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] += dpp_mov<0x142, 0xA>(v[r]);
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] += dpp_mov<0x143, 0xC>(v[r]);
+#pragma unroll
+    for (int r = 0; r < R; r++) v[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[r]), 63));
+}
+
+// ---- the loaders ----------------------------------------------------------------
+// Loader k issues the 64-unit instructions j = k, k + NLW, ... of the stream
+// [0, total): instruction j fills ring units (64 j mod RU) .. +63 (RU is a
+// multiple of 64, so an instruction never wraps).  An instruction may be
+// issued once every unit it overwrites is consumed: its last unit lies within
+// RU units of the consumed boundary (the least of the compute wavefronts'
+// counters).  A batch is LBATCH of the loader's next instructions; while the
+// ring has room, a loader keeps two batches in flight and publishes S.done[k]
+// as each lands; when it has not, the loader issues as many instructions as
+// fit and waits for them.
+//
+// Progress: a compute wavefront waits for a batch of up to R of its rows
+// (rows are dealt round-robin, stride NCW).  When every wavefront waits on
+// the ring, the wavefront with the lowest next row has a batch ending at most
+// NCW * R rows (or all the phase's rows) past the consumed boundary, so its
+// last instruction is issuable
+// whenever those rows plus one instruction fit in the ring (R = 4 rows of
+// width dim, 2 rows of width q_dim or ffn, 2 QKV row pairs); ring_fits checks
+// that.
+// The least of the compute wavefronts' consumed counters, read by a loader.
+// The reads are one inline-assembly block (reads, then the wait for them):
+// for an ordinary LDS read the compiler would first wait for every
+// direct-to-LDS load still in flight (they write LDS), which would serialize
+// the loader's batches.  The outputs are early-clobber and only used after the
+// block, so no result is read before its load has returned.
+static_assert(NCW == 4, "min_consumed reads four counters");
+__device__ __forceinline__ int min_consumed(const StepShared& S) {
+    unsigned addr[NCW];
+#pragma unroll
+    for (int w = 0; w < NCW; w++) addr[w] = (unsigned)(size_t)(const __attribute__((address_space(3))) int*)&S.cons[w];
+    int c0, c1, c2, c3;
+    asm volatile(
+        "ds_read_b32 %0, %4\n\t"
+        "ds_read_b32 %1, %5\n\t"
+        "ds_read_b32 %2, %6\n\t"
+        "ds_read_b32 %3, %7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(c0), "=&v"(c1), "=&v"(c2), "=&v"(c3)
+        : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3])
+        : "memory");
+    return __builtin_amdgcn_readfirstlane(min(min(c0, c1), min(c2, c3)));
+}
+
+// A loader's store of its done counter, as inline assembly: as an atomic
+// release store the compiler would first wait for every direct-to-LDS load in
+// flight, including the batch just issued.  The caller waits (s_waitcnt) for
+// the loads the counter covers.
+__device__ __forceinline__ void publish_done(StepShared& S, int k, int v) {
+    const unsigned addr = (unsigned)(size_t)(__attribute__((address_space(3))) int*)&S.done[k];
+    asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (lgkm and exp counters untouched).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+__device__ __forceinline__ void run_loader(StepShared& S, gptr<const uint8_t> stream, int total, int k, const Ctl& C) {
+    const int lane = threadIdx.x & 63;
+    const int n_instr = (total + 63) / 64;
+    auto issue = [&](int j0, int j1) {
+        for (int jj = j0; jj <= j1; jj += NLW) {
+            const int u = jj * 64 + lane;
+            if (u < total)
+                __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(stream + (size_t)u * 16),
+                                                 (__attribute__((address_space(3))) void*)(S.ring + ((jj * 64) % RU) * 16),
+                                                 16, 0, 0);
+        }
+    };
+    if (k < n_instr) {
+        const int last = n_instr - 1 - ((n_instr - 1 - k) % NLW);  // this loader's last instruction
+        int j = k;
+        int pend = -1;  // done value of the batch in flight (-1: none)
+        while (j <= last) {
+            // A full batch (LBATCH instructions) that fits behind the consumed
+            // boundary is issued while the previous one is still in flight;
+            // once it is issued, at most LBATCH instructions are outstanding
+            // when the previous batch has landed.
+            const int j_full = j + NLW * (LBATCH - 1);
+            if (j_full <= last && (j_full + 1) * 64 <= min_consumed(S) + RU) {
+                issue(j, j_full);
+                if (pend >= 0) {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(LBATCH));
+                    publish_done(S, k, pend);
                 }
-                isum -= 8 * A.sum[b];
+                pend = j = j_full + NLW;
+                continue;
             }
-            acc += sq_q_term(isum, A.s[b], sq_f16_to_f32(B.d[r][b]));
+            if (pend >= 0) {  // land what is in flight first
+                __builtin_amdgcn_s_waitcnt(0);
+                lds_release(&S.done[k], pend);
+                pend = -1;
+                continue;
+            }
+            // a partial batch: at least instruction j must be issuable; mc is
+            // the counter value that allowed it, so allowed >= j below
+            int mc = 0;
+            const bool ok = spin_lds(
+                [&] {
+                    mc = min_consumed(S);
+                    return (j + 1) * 64 <= mc + RU;
+                },
+                S, C);
+            if (!ok) {
+                lds_st(&S.abort, 1);
+                return;
+            }
+            const int allowed = (mc + RU) / 64 - 1;  // last issuable instruction
+            int j_last = min(j_full, last);
+            if (j_last > allowed) j_last = allowed - (allowed - j) % NLW;
+            j_last = max(j_last, j);  // j itself is issuable: every pass advances j
+            // a batch that is full after all goes through the pipelined path
+            if (j_last == j_full) continue;
+            issue(j, j_last);
+            __builtin_amdgcn_s_waitcnt(0);
+            j = j_last + NLW;
+            lds_release(&S.done[k], j);
         }
-        res[r] = sq_wave_sum(acc);
+        if (pend >= 0) {
+            __builtin_amdgcn_s_waitcnt(0);
+            lds_release(&S.done[k], pend);
+        }
     }
+    lds_release(&S.done[k], n_instr + NLW);
 }
 
-// Activation blocks from gathered exchange payloads: nblk blocks of 8 payload
-// words (32 int8) at S.xw[0..), then nblk scale words (f32 of the fp16 scale).
-template <int WT, int NBL>
-__device__ __forceinline__ void act_from_xw(Act<NBL>& A, const StepShared& S, int nblk, int lane) {
+// Units of the stream in the ring from the start (all instructions below the
+// least of the loaders' next instructions).
+__device__ __forceinline__ int filled_units(const StepShared& S) {
+    int d = lds_ld(&S.done[0]);
 #pragma unroll
-    for (int b = 0; b < NBL; b++) {
-        const int blk = lane + 64 * b;
-        if (blk < nblk) {
-#pragma unroll
-            for (int v = 0; v < 8; v++) A.q[b][v] = (int)S.xw[blk * 8 + v];
-            A.s[b] = __builtin_bit_cast(float, S.xw[nblk * 8 + blk]);
-        } else {
-#pragma unroll
-            for (int v = 0; v < 8; v++) A.q[b][v] = 0;
-            A.s[b] = 0.0f;
-        }
-        int s = 0;
-        if constexpr (WT == WT_Q4_0) {
-#pragma unroll
-            for (int v = 0; v < 8; v++) s = __builtin_amdgcn_sdot4(A.q[b][v], 0x01010101, s, false);
-        }
-        A.sum[b] = s;
-    }
+    for (int k = 1; k < NLW; k++) d = min(d, lds_ld(&S.done[k]));
+    return d * 64;
 }
 
-// One row against activation blocks gathered in S.xw (nblk blocks of 8
-// payload words, then nblk scale words), read from LDS as they are used.
-template <int WT, int NBL>
-__device__ __forceinline__ float dot_row_xw(const Rows<WT, NBL, 1>& B, const StepShared& S, int nblk, int lane) {
-    float acc = 0.0f;
+// ---- activations --------------------------------------------------------------
+// Norm gains of the 8 row elements a compute thread normalizes (elements
+// 8t .. 8t+7), requested before the phase's input gather so that both arrive
+// together.
+struct Gains {
+    sq_v4f v[2];
+};
+__device__ __forceinline__ Gains load_gains(const float* w, int D) {
+    const int t = threadIdx.x;  // < CNT
+    const gptr<const sq_v4f> wp = (gptr<const sq_v4f>)(gl(w) + (t < D / 8 ? t * 8 : 0));
+    Gains G;
+    G.v[0] = wp[0];
+    G.v[1] = wp[1];
+    return G;
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_int(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// RMSNorm (rms_norm.rs:40-56) of the hidden row and its Q8_0 quantization
+// (dot_prod.rs:21-31), spread over the compute group: thread t owns elements
+// 8t .. 8t+7 of the row.  They come from the exchange words src[8t ..] once
+// these carry `tag` (or, with src null, from the token's embedding row).  The
+// sum of squares is reduced per wavefront, then across the wavefronts in a
+// fixed order after a compute-group barrier; the four threads of a 32-block
+// (a lane quad) agree on its scale through DPP and the blocks land in
+// S.aq / S.as / S.asum.  Ends with a compute-group barrier; false: abandon.
+template <typename Embed>
+__device__ __forceinline__ bool norm_quant(StepShared& S, const u64* src, unsigned tag, Embed&& embed, const Gains& G,
+                                           int D, float eps, float* dbg_y, int8_t* dbg_q, uint16_t* dbg_d, int& gen,
+                                           const Ctl& C) {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));  // addresses formed in place (see gather)
+    const int lane = t & 63, cw = t >> 6;
+    const int KB = D >> 5;
+    const bool mine = t < 4 * KB;
+    float xs[8];
+    if (src != nullptr) {
+            const u64* p[8];
+        u64 w[8];
 #pragma unroll
-    for (int b = 0; b < NBL; b++) {
-        const int blk = lane + 64 * b;
-        if (blk >= nblk) continue;
-        const uint4* pq = (const uint4*)(S.xw + blk * 8);
-        const uint4 a0 = pq[0], a1 = pq[1];
-        const int aq[8] = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        const float sa = __builtin_bit_cast(float, S.xw[nblk * 8 + blk]);
-        int isum = 0;
-        if constexpr (WT == WT_Q8_0) {
-#pragma unroll
-            for (int v = 0; v < 8; v++) isum = __builtin_amdgcn_sdot4(aq[v], B.w[0][b][v], isum, false);
-        } else {
-            int asum = 0;
-#pragma unroll
-            for (int v = 0; v < 8; v++) asum = __builtin_amdgcn_sdot4(aq[v], 0x01010101, asum, false);
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int dw = B.w[0][b][v];
-                isum = __builtin_amdgcn_sdot4(aq[v], dw & 0x0F0F0F0F, isum, false);
-                isum = __builtin_amdgcn_sdot4(aq[4 + v], (dw >> 4) & 0x0F0F0F0F, isum, false);
-            }
-            isum -= 8 * asum;
+        for (int e = 0; e < 8; e++) {
+            p[e] = mine ? src + 8 * t + e : nullptr;
+            w[e] = mine ? ld_c(src + 8 * t + e) : 0;
         }
-        acc += sq_q_term(isum, sa, sq_f16_to_f32(B.d[0][b]));
+        if (!await_words(p, w, tag, C, &S.abort)) lds_st(&S.abort, 1);
+#pragma unroll
+        for (int e = 0; e < 8; e++) xs[e] = __builtin_bit_cast(float, (unsigned)w[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) xs[e] = mine ? embed(8 * t + e) : 0.0f;
     }
-    return sq_wave_sum(acc);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += mine ? xs[e] * xs[e] : 0.0f;
+    ss = wave_total(ss);
+    if (lane == 0) S.ssum[cw] = ss;
+    if (!csync(S, gen, C)) return false;
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NCW; w++) tot += S.ssum[w];
+    const float rms = sqrtf(tot / (float)D + eps);
+    if (mine) {
+        const float gs[8] = {G.v[0].x, G.v[0].y, G.v[0].z, G.v[0].w, G.v[1].x, G.v[1].y, G.v[1].z, G.v[1].w};
+        float y[8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            y[e] = (xs[e] * gs[e]) / rms;
+            amax = fmaxf(amax, fabsf(y[e]));
+        }
+        // the block's amax over its lane quad
+        amax = fmaxf(amax, __builtin_bit_cast(float, dpp_int<0xB1>(__builtin_bit_cast(int, amax))));
+        amax = fmaxf(amax, __builtin_bit_cast(float, dpp_int<0x4E>(__builtin_bit_cast(int, amax))));
+        const float sc = sq_q8_scale(amax);
+        const float inv = sq_q8_inv(sc);
+        int packed[2] = {0, 0};
+        int qsum = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int qv = sq_q8_quant(y[e], inv);
+            qsum += qv;
+            packed[e >> 2] |= (qv & 0xFF) << (8 * (e & 3));
+        }
+        qsum += dpp_int<0xB1>(qsum);
+        qsum += dpp_int<0x4E>(qsum);
+        const int blk = t >> 2;
+        *(int2*)&S.aq[2 * t] = make_int2(packed[0], packed[1]);
+        const uint16_t d16 = sq_f32_to_f16(sc);
+        if ((t & 3) == 0) {
+            S.as[blk] = sq_f16_to_f32(d16);
+            S.asum[blk] = qsum;
+        }
+        if (dbg_y) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                dbg_y[8 * t + e] = y[e];
+                dbg_q[8 * t + e] = (int8_t)((packed[e >> 2] >> (8 * (e & 3))) & 0xFF);
+            }
+            if ((t & 3) == 0) dbg_d[blk] = d16;
+        }
+    }
+    return csync(S, gen, C);
+}
+
+// The lane's activation block (block = lane) after norm_quant.
+__device__ __forceinline__ ActQ act_lane(const StepShared& S, int D) {
+    const int lane = threadIdx.x & 63;
+    const bool v = lane < (D >> 5);
+    const int b = v ? lane : 0;
+    const uint4* p = (const uint4*)&S.aq[8 * b];
+    const uint4 a0 = p[0], a1 = p[1];
+    ActQ A;
+    A.q[0] = v ? (int)a0.x : 0;
+    A.q[1] = v ? (int)a0.y : 0;
+    A.q[2] = v ? (int)a0.z : 0;
+    A.q[3] = v ? (int)a0.w : 0;
+    A.q[4] = v ? (int)a1.x : 0;
+    A.q[5] = v ? (int)a1.y : 0;
+    A.q[6] = v ? (int)a1.z : 0;
+    A.q[7] = v ? (int)a1.w : 0;
+    A.s = v ? S.as[b] : 0.0f;
+    A.sum = v ? S.asum[b] : 0;
+    return A;
+}
+
+// Activation block `blk` of gathered exchange payloads (nblk blocks of 8
+// payload words, then nblk scale words); zero past nblk.
+template <int WT>
+__device__ __forceinline__ ActQ xw_block(const unsigned* xw, int nblk, int blk) {
+    const bool v = blk < nblk;
+    const int b = v ? blk : 0;
+    const uint4* pq = (const uint4*)(xw + b * 8);
+    const uint4 a0 = pq[0], a1 = pq[1];
+    ActQ A;
+    A.q[0] = v ? (int)a0.x : 0;
+    A.q[1] = v ? (int)a0.y : 0;
+    A.q[2] = v ? (int)a0.z : 0;
+    A.q[3] = v ? (int)a0.w : 0;
+    A.q[4] = v ? (int)a1.x : 0;
+    A.q[5] = v ? (int)a1.y : 0;
+    A.q[6] = v ? (int)a1.z : 0;
+    A.q[7] = v ? (int)a1.w : 0;
+    A.s = v ? __builtin_bit_cast(float, xw[nblk * 8 + b]) : 0.0f;
+    A.sum = 0;
+    if constexpr (WT == WT_Q4_0) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) A.sum = __builtin_amdgcn_sdot4(A.q[k], 0x01010101, A.sum, false);
+    }
+    return A;
 }
 
 // Quantize 32-element blocks held one element per lane (lanes 0..31 and
@@ -328,86 +709,6 @@ __device__ __forceinline__ void quant_put(float v, int lane, int block0, u64* q,
     if ((lane & 31) == 0 && valid) putf(s + blk, sq_f16_to_f32(sq_f32_to_f16(sc)), tag);
 }
 
-// RMSNorm of a D-wide row (x: EPT elements per thread, indexes tid + j*SNT)
-// and Q8_0 quantization into S.qs / S.d (rms_norm.rs:40-56, dot_prod.rs:21-31).
-constexpr int EPT = DMAX / SNT;
-// Norm gains of the row elements a thread owns, requested ahead of the
-// phase's input gather so both arrive together.
-__device__ __forceinline__ void load_gains(float (&nw)[EPT], const float* w, int D) {
-#pragma unroll
-    for (int j = 0; j < EPT; j++) {
-        const int i = threadIdx.x + j * SNT;
-        nw[j] = i < D ? gl(w)[i] : 0.0f;
-    }
-}
-
-template <int WT>
-__device__ __forceinline__ void norm_quant(StepShared& S, const float (&x)[EPT], const float (&nw)[EPT], int D,
-                                           float eps, float* dbg_y, int8_t* dbg_q, uint16_t* dbg_d) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < EPT; j++) ss += x[j] * x[j];
-    ss = sq_wave_sum(ss);
-    if (lane == 0) S.red[wave] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int k = 0; k < SW; k++) tot += S.red[k];
-    const float rms = sqrtf(tot / (float)D + eps);
-#pragma unroll
-    for (int j = 0; j < EPT; j++) {
-        const int i = tid + j * SNT;
-        const bool vi = i < D;
-        const float y = vi ? (x[j] * nw[j]) / rms : 0.0f;
-        const float amax = fmaxf(sq_half_max(fabsf(y)), 0.0f);
-        const float sc = sq_q8_scale(amax);
-        const int8_t q = sq_q8_quant(y, sq_q8_inv(sc));
-        if (vi) {
-            S.qs[i] = q;
-            if ((i & 31) == 0) S.d[i >> 5] = sq_f32_to_f16(sc);
-            if (dbg_y) {
-                dbg_y[i] = y;
-                dbg_q[i] = q;
-                if ((i & 31) == 0) dbg_d[i >> 5] = sq_f32_to_f16(sc);
-            }
-        }
-        if constexpr (WT == WT_Q4_0) {
-            int qi = q;
-#pragma unroll
-            for (int o = 16; o >= 1; o >>= 1) qi += __shfl_xor(qi, o, 64);
-            if (vi && (i & 31) == 0) S.asum[i >> 5] = qi;
-        }
-    }
-    __syncthreads();
-}
-
-template <int WT>
-__device__ __forceinline__ void act_from_lds(Act<1>& A, const StepShared& S, int KB, int lane) {
-    if (lane < KB) {
-        const int4* p = (const int4*)(S.qs + lane * 32);
-        const int4 x0 = p[0], x1 = p[1];
-        A.q[0][0] = x0.x; A.q[0][1] = x0.y; A.q[0][2] = x0.z; A.q[0][3] = x0.w;
-        A.q[0][4] = x1.x; A.q[0][5] = x1.y; A.q[0][6] = x1.z; A.q[0][7] = x1.w;
-        A.s[0] = sq_f16_to_f32(S.d[lane]);
-        A.sum[0] = (WT == WT_Q4_0) ? S.asum[lane] : 0;
-    } else {
-#pragma unroll
-        for (int v = 0; v < 8; v++) A.q[0][v] = 0;
-        A.s[0] = 0.0f;
-        A.sum[0] = 0;
-    }
-}
-
-// Gathered hidden row -> x[] (element tid + j*SNT).
-__device__ __forceinline__ void x_from_xw(float (&x)[EPT], const StepShared& S, int D) {
-#pragma unroll
-    for (int j = 0; j < EPT; j++) {
-        const int i = threadIdx.x + j * SNT;
-        x[j] = i < D ? __builtin_bit_cast(float, S.xw[i]) : 0.0f;
-    }
-}
-
 __device__ __forceinline__ void arg_merge(float& bv, int& bi, int& bn, float v, int i, int n) {
     if (i >= 0 && (bi < 0 || v > bv || (v == bv && i > bi))) {
         bv = v;
@@ -416,8 +717,7 @@ __device__ __forceinline__ void arg_merge(float& bv, int& bi, int& bn, float v, 
     bn = n > bn ? n : bn;
 }
 
-__device__ __forceinline__ void block_arg(StepShared& S, float& bv, int& bi, int& bn) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ void wave_arg(float& bv, int& bi, int& bn) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
@@ -425,39 +725,55 @@ __device__ __forceinline__ void block_arg(StepShared& S, float& bv, int& bi, int
         const int on = __shfl_xor(bn, o, 64);
         arg_merge(bv, bi, bn, ov, oi, on);
     }
-    __syncthreads();
-    if (lane == 0) {
-        S.bv[wave] = bv;
-        S.bi[wave] = bi;
-        S.bn[wave] = bn;
-    }
-    __syncthreads();
-    bv = S.bv[0];
-    bi = S.bi[0];
-    bn = S.bn[0];
-    for (int w = 1; w < SW; w++) arg_merge(bv, bi, bn, S.bv[w], S.bi[w], S.bn[w]);
 }
 
 // Phase tags: layer l, phase j in [0, 6): QKV, attention, tile merge, o, gate/up, down.
 enum : int { PH_QKV = 0, PH_ATTN = 1, PH_MERGE = 2, PH_O = 3, PH_GU = 4, PH_DOWN = 5, PH_PER_LAYER = 6 };
 // Timeline slots of one layer (optional measurement).
 enum TraceSlot : int {
-    TS_QKV_IN = 0, TS_QKV = 1, TS_ATTN = 2, TS_MERGE = 3, TS_O_IN = 4, TS_O = 5, TS_GU_IN = 6, TS_GU_DOT = 7,
-    TS_GU = 8, TS_DOWN_IN = 9, TS_DOWN = 10, TS_PER_LAYER = 16
+    TS_QKV_IN = 0,  // QKV input row gathered, normalized and quantized
+    TS_QKV = 1, TS_ATTN = 2, TS_MERGE = 3, TS_O_IN = 4, TS_O = 5, TS_GU_IN = 6, TS_GU_DOT = 7,
+    TS_GU = 8, TS_DOWN_IN = 9, TS_DOWN = 10,
+    TS_ATT_Q = 11,     // attention: q and the new K/V row gathered (first item)
+    TS_ATT_S = 12,     // attention: scores done (first item)
+    TS_ATT_PV = 13,    // attention: outputs published (first item)
+    TS_RING_GU = 14,   // ticks wavefront 0 waited on the ring in the gate/up phase (a duration)
+    TS_RING_ALL = 15,  // ticks wavefront 0 waited on the ring in the layer (a duration)
+    TS_QKV_NORM = 16,  // QKV: quantized activation read back
+    TS_GU_NORM = 17,   // gate/up: quantized activation read back
+    TS_PER_LAYER = 20
 };
 
 template <int WT>
 __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     __shared__ StepShared S;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wavefront index is uniform; readfirstlane lets the compiler keep
+    // everything derived from it (roles, row loops) in scalar registers
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int G = gridDim.x, wg = blockIdx.x;
-    const int NW = G * SW;             // wavefronts in the launch
-    const int gw = wg * SW + wave;     // this wavefront's global index
     const int D = a.dim, F = a.ffn;
     const int QD = a.n_heads * HDIM, KVD = a.n_kv_heads * HDIM;
     const int KB = D >> 5;
     const int GQ = a.n_heads / a.n_kv_heads;
     const Ctl C{a.error, a.spin_limit};
+    const StreamGeo g = stream_geo(WT, a.n_layers, D, F, QD, KVD, a.vocab, G, wg);
+
+    if (tid == 0) {
+        S.abort = 0;
+        S.csync = 0;
+    }
+    if (tid < NLW) S.done[tid] = 0;
+    if (tid < NCW) S.cons[tid] = 0;
+    if (a.trace && tid == 0) a.trace[(size_t)wg * a.trace_stride] = wall_clock64();
+    __syncthreads();  // the workgroup's only full barrier
+
+    if (wave >= NCW) {
+        run_loader(S, gl((const uint8_t*)a.stream) + (size_t)wg * a.stream_stride * 16, g.total, wave - NCW, C);
+        return;
+    }
+
+    // ------------------------------------------------------------ compute group
+    const int cw = wave;  // 0..NCW-1
     const unsigned epoch = *a.epoch;
     auto tag = [&](int l, int ph) -> unsigned { return epoch + 1u + (unsigned)(l * PH_PER_LAYER + ph); };
     const unsigned head_tag = epoch + 1u + (unsigned)(a.n_layers * PH_PER_LAYER);
@@ -465,24 +781,72 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     const uint32_t tok = *a.token;
     const int P = pos + 1;
     const int ntiles = (P + TPOS - 1) / TPOS;
-    const int nchunks = (ntiles + CHUNK - 1) / CHUNK;
     const Xchg X = a.x;
-    if (tid == 0) S.abort = 0;
-    if (a.trace && tid == 0) a.trace[(size_t)wg * a.trace_stride] = wall_clock64();
-    __syncthreads();
-    // timeline slots per layer (measurement): see TraceSlot
+    const cptr<StepLayer> LY = (cptr<StepLayer>)a.layers;
+    int gen = 0;  // compute-group barrier count
+    auto next_xw = [&]() -> unsigned* { return S.xw; };
+
     auto stamp = [&](int l, int slot) {
         if (a.trace && tid == 0) {
             const int k = 1 + l * TS_PER_LAYER + slot;
             if (k < a.trace_stride) a.trace[(size_t)wg * a.trace_stride + k] = wall_clock64();
         }
     };
+    auto put_duration = [&](int l, int slot, long long v) {
+        if (a.trace && tid == 0) {
+            const int k = 1 + l * TS_PER_LAYER + slot;
+            if (k < a.trace_stride) a.trace[(size_t)wg * a.trace_stride + k] = (unsigned long long)v;
+        }
+    };
+    auto fail = [&]() { lds_st(&S.abort, 1); };
+    // Ring fill level as last read (wave-uniform).  ensure(end) returns once
+    // the ring holds stream units below `end`, reading the loaders' counters
+    // only when the cached level falls short (when tracing, the time waited
+    // is added to ring_wait).
+    int filled_c = 0;
+    long long ring_wait = 0;
+    auto ensure = [&](int end) -> bool {
+        if (filled_c >= end) return true;
+        const long long t = a.trace ? wall_clock64() : 0;
+        const bool ok = spin_lds(
+            [&] {
+                filled_c = __builtin_amdgcn_readfirstlane(filled_units(S));
+                return filled_c >= end;
+            },
+            S, C);
+        if (a.trace) ring_wait += wall_clock64() - t;
+        return ok;
+    };
+    // this wavefront is done with every own row ending at or below `end`
+    auto consumed = [&](int end) {
+        if (lane == 0) lds_release(&S.cons[cw], end);
+    };
+    // ring position of stream unit u (u is wave-uniform)
+    auto ring_pos = [&](int u) -> unsigned { return (unsigned)__builtin_amdgcn_readfirstlane(u % RU); };
 
-    const int q_units = (QD + 2 * KVD) / 2;   // RoPE pairs of the stacked QKV rows
-    const int gu_tiles = F / 32;
+    // Dot products of this wavefront's rows i = cw + NCW * (r0 + r), r < n
+    // (n <= R), of a phase whose row i occupies stream units base + i*ru ..,
+    // against activation A (one 32-block per lane, lanes below kb).  All rows'
+    // reads are issued before any reduction.  False: abandon.
+    auto dot_batch = [&](auto Rc, int base, int ru, int pu, int r0, int n, int kb, const ActQ& A, float* res) -> bool {
+        constexpr int R = decltype(Rc)::value;
+        if (!ensure(base + (cw + NCW * (r0 + n - 1) + 1) * ru)) return false;
+        // rows past n re-read the batch's first row (in the ring; discarded)
+        RowData rd[R];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            rd[r] = row_fetch<WT>(S, ring_pos(base + (cw + NCW * (r0 + (r < n ? r : 0))) * ru), pu, lane);
+        float t[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) t[r] = row_math<WT>(rd[r], A, lane < kb);
+        wave_totals(t);
+#pragma unroll
+        for (int r = 0; r < R; r++) res[r] = t[r];
+        return true;
+    };
 
-    // The residual row this wavefront owns (hidden[gw]), from the embedding
-    // of the token (embed, model.rs:57-62; dequantize_into is exact).
+    // Residual rows owned: o/down rows i = cw + NCW r of this CU, from the
+    // embedding of the token (embed, model.rs:57-62; dequantize_into is exact).
     auto embed_at = [&](int i) -> float {
         const float sc = sq_f16_to_f32(gl(a.embd.scale)[(size_t)tok * KB + (i >> 5)]);
         if constexpr (WT == WT_Q8_0) {
@@ -494,413 +858,452 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
             return sc * (float)(q - 8);
         }
     };
-    float h_own = gw < D ? embed_at(gw) : 0.0f;
-
-    float x[EPT];
-    Rows<WT, 1, 2> Wq;
-    Rows<WT, 1, 1> Wo;
-    Rows<WT, 1, 8> Wg;
-    Rows<WT, 4, 1> Wd;
-    Rows<WT, 1, 4> Wh0, Wh1;
-
-    auto qkv_rows = [&](int u, int (&rr)[2]) {
-        rr[0] = u < q_units ? 2 * u : -1;
-        rr[1] = u < q_units ? 2 * u + 1 : -1;
-    };
-    auto gu_rows = [&](int t, int (&rr)[8]) {
+    float h_own[RMAX];
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const int slot = wave * 8 + r;
-            rr[r] = t < gu_tiles ? (slot < 32 ? t * 32 + slot : F + t * 32 + (slot - 32)) : -1;
-        }
-    };
-    auto head_rows = [&](int u, int (&rr)[4]) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) rr[r] = (4 * u + r < a.vocab) ? 4 * u + r : -1;
-    };
-    const cptr<StepLayer> LY = (cptr<StepLayer>)a.layers;
-    float nw[EPT];
-    {
-        int rr[2];
-        qkv_rows(gw, rr);
-        const MatView m0 = view_of(LY[0].qkv);
-        load_rows(Wq, m0, rr, lane);
+    for (int r = 0; r < RMAX; r++) {
+        const int i = cw + NCW * r;
+        const int row = g.row0o + i;
+        h_own[r] = (i < g.no && row < D) ? embed_at(row) : 0.0f;
     }
+    // rows of o/down this wavefront owns (i = cw, cw + NCW)
+    const int n_own = g.no > cw + NCW ? 2 : (g.no > cw ? 1 : 0);
 
     for (int l = 0; l < a.n_layers; l++) {
-
+        const int lb = l * g.LU;  // first unit of the layer
         const gptr<float> kc = gl(a.kcache + (size_t)l * a.kv_layer);
         const gptr<float> vc = gl(a.vcache + (size_t)l * a.kv_layer);
 
         // ------------------------------------------------ QKV + RoPE + KV append
         {
             const unsigned T = tag(l, PH_QKV);
-            const bool work = wg * SW < q_units;
-            // RoPE (cos, sin) of this wavefront's row pair, requested early
-            float rc = 1.0f, rs = 0.0f;
-            if (gw < q_units && 2 * gw < QD + KVD) {
-                const int li = 2 * gw < QD ? 2 * gw : 2 * gw - QD;
-                const gptr<const float> cs =
-                    gl((const float*)a.rope) + 2 * ((size_t)pos * (HDIM / 2) + ((li % HDIM) >> 1));
-                rc = cs[0];
-                rs = cs[1];
-            }
-            if (work) {
-                load_gains(nw, LY[l].attn_norm, D);
-                if (l == 0) {
+            if (g.row0q < QD + 2 * KVD) {
+                // this wavefront's row pairs p = cw + NCW r (r < 2) and their
+                // RoPE (cos, sin), requested before the input gather
+                const int np = g.nq / 2 > cw + NCW ? 2 : (g.nq / 2 > cw ? 1 : 0);
+                float rc[2] = {1.0f, 1.0f}, rs[2] = {0.0f, 0.0f};
 #pragma unroll
-                    for (int j = 0; j < EPT; j++) {
-                        const int i = tid + j * SNT;
-                        x[j] = i < D ? embed_at(i) : 0.0f;
+                for (int r = 0; r < 2; r++) {
+                    const int row = g.row0q + 2 * (cw + NCW * r);
+                    if (r < np && row < QD + KVD) {
+                        const int li = row < QD ? row : row - QD;
+                        const cptr<float> cs =
+                            (cptr<float>)a.rope + 2 * ((size_t)pos * (HDIM / 2) + ((li % HDIM) >> 1));
+                        rc[r] = cs[0];
+                        rs[r] = cs[1];
                     }
-                } else {
-                    if (!gather(S, X.h, D, tag(l - 1, PH_DOWN), C)) return;
-                    x_from_xw(x, S, D);
                 }
-            }
-            stamp(l, TS_QKV_IN);
-            if (work) {
+                const Gains gn = load_gains(LY[l].attn_norm, D);
                 const bool dbg = l == 0 && wg == 0 && a.dbg_normed != nullptr;
-                norm_quant<WT>(S, x, nw, D, a.eps, dbg ? a.dbg_normed : nullptr, a.dbg_qs, a.dbg_d);
-                Act<1> A;
-                act_from_lds<WT>(A, S, KB, lane);
-                if (gw < q_units) {
-                    const int u = gw;
-                    float res[2];
-                    dot_rows<WT, 1, 2>(Wq, A, KB, lane, res);
-                    if (lane == 0) {
-                        const int row = 2 * u;
-                        if (row < QD + KVD) {
-                            const bool is_q = row < QD;
-                            const int li = is_q ? row : row - QD;
-                            float o0, o1;
-                            sq_rotate(res[0], res[1], rc, rs, o0, o1);
-                            if (is_q) {
-                                putf(X.q + li, o0, T);
-                                putf(X.q + li + 1, o1, T);
+                if (!norm_quant(S, l == 0 ? nullptr : X.h, l == 0 ? 0u : tag(l - 1, PH_DOWN), embed_at, gn, D, a.eps,
+                                dbg ? a.dbg_normed : nullptr, a.dbg_qs, a.dbg_d, gen, C))
+                    return;
+                stamp(l, TS_QKV_IN);
+                const ActQ A = act_lane(S, D);
+                stamp(l, TS_QKV_NORM);
+                const int pu = stream_row_units(WT, D) - D / 256;
+                if (np > 0) {
+                    // a pair is two consecutive rows: 2 * ua units
+                    if (!ensure(lb + (cw + NCW * (np - 1) + 1) * 2 * g.ua)) return fail();
+                    RowData rd[4];
+#pragma unroll
+                    for (int r = 0; r < 2; r++) {
+                        const unsigned rb = ring_pos(lb + 2 * (cw + NCW * (r < np ? r : 0)) * g.ua);
+                        rd[2 * r] = row_fetch<WT>(S, rb, pu, lane);
+                        rd[2 * r + 1] = row_fetch<WT>(S, ring_wrap(rb + g.ua), pu, lane);
+                    }
+                    float tt[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) tt[k] = row_math<WT>(rd[k], A, lane < KB);
+                    wave_totals(tt);
+#pragma unroll
+                    for (int r = 0; r < 2; r++) {
+                        if (r >= np) continue;
+                        const float r0 = tt[2 * r], r1 = tt[2 * r + 1];
+                        const int row = g.row0q + 2 * (cw + NCW * r);
+                        if (lane == 0 && row < QD + 2 * KVD) {
+                            if (row < QD + KVD) {
+                                const bool is_q = row < QD;
+                                const int li = is_q ? row : row - QD;
+                                float o0, o1;
+                                sq_rotate(r0, r1, rc[r], rs[r], o0, o1);
+                                if (is_q) {
+                                    putf(X.q + li, o0, T);
+                                    putf(X.q + li + 1, o1, T);
+                                } else {
+                                    kc[(size_t)pos * KVD + li] = o0;
+                                    kc[(size_t)pos * KVD + li + 1] = o1;
+                                    putf(X.k + li, o0, T);
+                                    putf(X.k + li + 1, o1, T);
+                                }
                             } else {
-                                kc[(size_t)pos * KVD + li] = o0;
-                                kc[(size_t)pos * KVD + li + 1] = o1;
-                                putf(X.k + li, o0, T);
-                                putf(X.k + li + 1, o1, T);
+                                const int li = row - QD - KVD;
+                                vc[(size_t)pos * KVD + li] = r0;
+                                vc[(size_t)pos * KVD + li + 1] = r1;
+                                putf(X.v + li, r0, T);
+                                putf(X.v + li + 1, r1, T);
                             }
-                        } else {
-                            const int li = row - QD - KVD;
-                            vc[(size_t)pos * KVD + li] = res[0];
-                            vc[(size_t)pos * KVD + li + 1] = res[1];
-                            putf(X.v + li, res[0], T);
-                            putf(X.v + li + 1, res[1], T);
                         }
                     }
                 }
             }
-            // the o-projection row of this wavefront, requested after the
-            // outputs are out (registers of pending loads would hold them up)
-            {
-                const int rr[1] = {gw < D ? gw : -1};
-                const MatView mv = view_of(LY[l].o);
-                load_rows(Wo, mv, rr, lane);
-            }
+            consumed(lb + g.offo);
             stamp(l, TS_QKV);
         }
 
         // ------------------------------------------------ attention (GQA)
-        // Work item = (kv head, chunk of tiles): one 64-position tile per item
-        // (CHUNK = 1); the partials of a head merge across workgroups.
+        // Work item = (kv head, 64-position tile).  Wavefront cw < GQ takes
+        // query head gh*GQ + cw on its own: lane = position for the scores
+        // (its K row in registers, q[d] read from lane d), lane = dimension
+        // for the output (its V column in registers, p read from lane
+        // `position`).  Cached rows (positions < pos) come from the KV cache,
+        // the new rows from this launch's exchange words; the new K row
+        // reaches its lane through a 64-word scratch of the wavefront in xw.
         {
             const unsigned Tin = tag(l, PH_QKV), T = tag(l, PH_ATTN);
-            const int items = a.n_kv_heads * nchunks;
+            const int items = a.n_kv_heads * ntiles;
             const float scale = 1.0f / sqrtf((float)HDIM);
             for (int it = wg; it < items; it += G) {
-                const int g = it / nchunks, tile = it % nchunks;
+                const int gh = it / ntiles, tile = it % ntiles;
                 const int s0 = tile * TPOS;
                 const bool cur = s0 + TPOS > pos;  // this tile holds the new position
-                // q of the group's heads and, in the last tile, the new K/V row
-                {
-                    const int nq = GQ * HDIM;
-                    const int n = nq + (cur ? 2 * HDIM : 0);
-                    bool ok = true;
-                    for (int e = tid; e < n; e += SNT) {
-                        const u64* src = e < nq ? X.q + (size_t)g * nq + e
-                                                : (e < nq + HDIM ? X.k + g * HDIM + (e - nq) : X.v + g * HDIM + (e - nq - HDIM));
-                        u64 w = ld_c(src);
-                        if (!await_word(src, w, Tin, C)) {
-                            ok = false;
-                            break;
-                        }
-                        const float f = __builtin_bit_cast(float, (unsigned)w);
-                        if (e < nq) S.qh[e / HDIM][e % HDIM] = f;
-                        else if (e < nq + HDIM) S.k[pos - s0][e - nq] = f;
-                        else S.v[pos - s0][e - nq - HDIM] = f;
-                    }
-                    if (!ok) S.abort = 1;
+                if (cw >= GQ) continue;
+                const int h = gh * GQ + cw;
+                // K row of position s0 + lane and V column `lane` of the tile
+                // (row 0 stands in for positions without a cached row; their
+                // scores are masked and their V values replaced below)
+                const bool cached = s0 + lane < pos;
+                const gptr<const sq_v4f> kp =
+                    (gptr<const sq_v4f>)(kc + (size_t)(cached ? s0 + lane : 0) * KVD + gh * HDIM);
+                sq_v4f kr[HDIM / 4];
+#pragma unroll
+                for (int i = 0; i < HDIM / 4; i++) kr[i] = kp[i];
+                // q[lane] of head h and, in the last tile, the new K/V rows' element lane
+                int t = tid;
+                asm volatile("" : "+v"(t));
+                const int d = t & 63;
+                const u64* pw[3] = {X.q + (size_t)h * HDIM + d, cur ? X.k + gh * HDIM + d : nullptr,
+                                    cur ? X.v + gh * HDIM + d : nullptr};
+                u64 w[3];
+#pragma unroll
+                for (int j = 0; j < 3; j++) w[j] = pw[j] ? ld_c(pw[j]) : 0;
+                if (!await_words(pw, w, Tin, C, &S.abort)) return fail();
+                const float vn = __builtin_bit_cast(float, (unsigned)w[2]);
+                unsigned* scr = S.xw + cw * HDIM;  // the new K row
+                scr[lane] = (unsigned)w[1];
+                __builtin_amdgcn_wave_barrier();
+                if (it == wg) stamp(l, TS_ATT_Q);
+                if (s0 + lane == pos) {
+#pragma unroll
+                    for (int i = 0; i < HDIM / 4; i++) kr[i] = *(const sq_v4f*)(scr + 4 * i);
                 }
-                for (int e = tid; e < TPOS * HDIM / 4; e += SNT) {
-                    const int r = e / (HDIM / 4), c4 = e % (HDIM / 4);
-                    const int sp = s0 + r;
-                    if (sp == pos) continue;  // gathered above
-                    float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
-                    if (sp < pos) {
-                        const size_t off = (size_t)sp * KVD + g * HDIM + 4 * c4;
-                        const sq_v4f kk = *(gptr<const sq_v4f>)(kc + off);
-                        const sq_v4f vv = *(gptr<const sq_v4f>)(vc + off);
-                        k4 = make_float4(kk.x, kk.y, kk.z, kk.w);
-                        v4 = make_float4(vv.x, vv.y, vv.z, vv.w);
-                    }
-                    S.k[r][4 * c4 + 0] = k4.x;
-                    S.k[r][4 * c4 + 1] = k4.y;
-                    S.k[r][4 * c4 + 2] = k4.z;
-                    S.k[r][4 * c4 + 3] = k4.w;
-                    *(float4*)&S.v[r][4 * c4] = v4;
-                }
-                __syncthreads();
-                if (S.abort) return;
                 // scores = dot(q, k) * (1/sqrt(head_dim)) (attention.rs:52-55)
-                for (int idx = tid; idx < GQ * TPOS; idx += SNT) {
-                    const int i = idx / TPOS, sp = idx % TPOS;
-                    float dot = 0.0f;
-#pragma unroll 16
-                    for (int d = 0; d < HDIM; d++) dot += S.qh[i][d] * S.k[sp][d];
-                    S.p[i][sp] = (s0 + sp < P) ? dot * scale : -INFINITY;
+                const float qv = __builtin_bit_cast(float, (unsigned)w[0]);
+                float dot = 0.0f;
+#pragma unroll
+                for (int i = 0; i < HDIM / 4; i++) {
+                    dot += lane_value(qv, 4 * i + 0) * kr[i].x;
+                    dot += lane_value(qv, 4 * i + 1) * kr[i].y;
+                    dot += lane_value(qv, 4 * i + 2) * kr[i].z;
+                    dot += lane_value(qv, 4 * i + 3) * kr[i].w;
                 }
-                __syncthreads();
-                if (wave < GQ) {
-                    const float v = S.p[wave][lane];
-                    const float m = sq_wave_max(v);
-                    const float p = (v == -INFINITY) ? 0.0f : expf(v - m);
-                    const float sum = sq_wave_sum(p);
-                    S.p[wave][lane] = p;
+                const float v = (s0 + lane < P) ? dot * scale : -INFINITY;
+                if (it == wg) stamp(l, TS_ATT_S);
+                const float m = wave_maximum(v);
+                const float pr = (v == -INFINITY) ? 0.0f : expf(v - m);
+                const float sum = wave_total(pr);
+                // V column `lane` of the tile (issued once the scores are done:
+                // with the K row also live it would not fit in registers)
+                float vv[TPOS];
+#pragma unroll
+                for (int sp = 0; sp < TPOS; sp++) {
+                    // row pointer uniform, lane offset in a register: scalar-base loads
+                    const gptr<const float> vrow = vc + (size_t)(s0 + sp < pos ? s0 + sp : 0) * KVD + gh * HDIM;
+                    vv[sp] = vrow[lane];
+                }
+                // o[lane] = sum over positions of p * v (lane = dimension)
+                float o = 0.0f;
+#pragma unroll
+                for (int sp = 0; sp < TPOS; sp++) {
+                    const float vs = s0 + sp < pos ? vv[sp] : (s0 + sp == pos ? vn : 0.0f);
+                    o += lane_value(pr, sp) * vs;
+                }
+                if (ntiles == 1) {
+                    quant_put(o / sum, lane, h * 2, X.a, X.a + QD / 4, T, true);
+                } else {
+                    // partial (o[64], m, l) of head h, tile `tile`
+                    u64* pt = X.t + ((size_t)h * a.max_tiles + tile) * (HDIM + 2);
+                    putf(pt + lane, o, T);
                     if (lane == 0) {
-                        S.m[wave] = m;
-                        S.l[wave] = sum;
+                        putf(pt + HDIM, m, T);
+                        putf(pt + HDIM + 1, sum, T);
                     }
                 }
-                __syncthreads();
-                if (wave < GQ) {
-                    const int h = g * GQ + wave, d = lane;
-                    float o = 0.0f;
-#pragma unroll 16
-                    for (int sp = 0; sp < TPOS; sp++) o += S.p[wave][sp] * S.v[sp][d];
-                    if (nchunks == 1) {
-                        quant_put(o / S.l[wave], lane, h * 2, X.a, X.a + QD / 4, T, true);
-                    } else {
-                        // partial (o[64], m, l) of head h, tile `tile`
-                        u64* pt = X.t + ((size_t)h * a.max_tiles + tile) * (HDIM + 2);
-                        putf(pt + d, o, T);
-                        if (lane == 0) {
-                            putf(pt + HDIM, S.m[wave], T);
-                            putf(pt + HDIM + 1, S.l[wave], T);
-                        }
-                    }
-                }
-                __syncthreads();
+                if (it == wg) stamp(l, TS_ATT_PV);
             }
+            // the scratch in xw is free again before the o gather writes xw
+            if (wg < items && !csync(S, gen, C)) return;
             stamp(l, TS_ATTN);
-            if (nchunks > 1) {
+            if (ntiles > 1) {
                 // merge the tiles of each head, then quantize the row
                 const unsigned Tm = tag(l, PH_MERGE);
                 bool ok = true;
-                for (int h = gw; h < a.n_heads && ok; h += NW) {
+                for (int h = wg * NCW + cw; h < a.n_heads && ok; h += G * NCW) {
                     const int d = lane;
                     float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
-                    for (int t0 = 0; t0 < nchunks && ok; t0 += 2) {
-                        u64 wo[2], wm[2], wl[2];
+                    for (int t0 = 0; t0 < ntiles && ok; t0 += 2) {
+                        // (o[d], m, l) of tiles t0 and t0 + 1
+                        const u64* pw[6];
+                        u64 w[6];
 #pragma unroll
-                        for (int j = 0; j < 2; j++) {
-                            const u64* pt = X.t + ((size_t)h * a.max_tiles + t0 + j) * (HDIM + 2);
-                            if (t0 + j < nchunks) {
-                                wo[j] = ld_c(pt + d);
-                                wm[j] = ld_c(pt + HDIM);
-                                wl[j] = ld_c(pt + HDIM + 1);
-                            }
+                        for (int j2 = 0; j2 < 2; j2++) {
+                            const u64* pt = X.t + ((size_t)h * a.max_tiles + t0 + j2) * (HDIM + 2);
+                            const bool v = t0 + j2 < ntiles;
+                            pw[3 * j2 + 0] = v ? pt + d : nullptr;
+                            pw[3 * j2 + 1] = v ? pt + HDIM : nullptr;
+                            pw[3 * j2 + 2] = v ? pt + HDIM + 1 : nullptr;
                         }
 #pragma unroll
-                        for (int j = 0; j < 2; j++) {
-                            if (t0 + j >= nchunks || !ok) continue;
-                            const u64* pt = X.t + ((size_t)h * a.max_tiles + t0 + j) * (HDIM + 2);
-                            ok = await_word(pt + d, wo[j], T, C) && await_word(pt + HDIM, wm[j], T, C) &&
-                                 await_word(pt + HDIM + 1, wl[j], T, C);
-                            if (!ok) continue;
-                            const float mt = __builtin_bit_cast(float, (unsigned)wm[j]);
+                        for (int j = 0; j < 6; j++) w[j] = pw[j] ? ld_c(pw[j]) : 0;
+                        ok = await_words(pw, w, T, C, &S.abort);
+                        if (!ok) continue;
+#pragma unroll
+                        for (int j2 = 0; j2 < 2; j2++) {
+                            if (t0 + j2 >= ntiles) continue;
+                            const float mt = __builtin_bit_cast(float, (unsigned)w[3 * j2 + 1]);
                             if (mt == -INFINITY) continue;
                             const float Mn = fmaxf(M, mt);
                             const float es = (M == -INFINITY) ? 0.0f : expf(M - Mn);
                             const float et = expf(mt - Mn);
-                            Lsum = Lsum * es + __builtin_bit_cast(float, (unsigned)wl[j]) * et;
-                            O = O * es + __builtin_bit_cast(float, (unsigned)wo[j]) * et;
+                            Lsum = Lsum * es + __builtin_bit_cast(float, (unsigned)w[3 * j2 + 2]) * et;
+                            O = O * es + __builtin_bit_cast(float, (unsigned)w[3 * j2]) * et;
                             M = Mn;
                         }
                     }
-                    // lanes of one wavefront agree on ok (each waits on its own
-                    // word; any failure aborts the launch)
+                    // lanes of one wavefront agree on ok (any failure aborts)
                     if (__all(ok)) quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, Tm, true);
                     else ok = false;
                 }
-                if (!ok) S.abort = 1;
-                __syncthreads();
-                if (S.abort) return;
+                if (!ok) return fail();
                 stamp(l, TS_MERGE);
             }
         }
 
         // ------------------------------------------------ o-projection + residual
         {
-            const unsigned Tin = tag(l, nchunks > 1 ? PH_MERGE : PH_ATTN), T = tag(l, PH_O);
-            const bool work = wg * SW < D;
+            const unsigned Tin = tag(l, ntiles > 1 ? PH_MERGE : PH_ATTN), T = tag(l, PH_O);
             const int QB = QD >> 5;
-            if (work && !gather(S, X.a, QD / 4 + QB, Tin, C)) return;
-            stamp(l, TS_O_IN);
-            if (work && gw < D) {
-                h_own += dot_row_xw<WT, 1>(Wo, S, QB, lane);  // elementwise_add (layers.rs:81-109)
-                if (lane == 0) putf(X.h + gw, h_own, T);
+            if (g.row0o < D) {
+                unsigned* xw = next_xw();
+                if (!gather(S, xw, X.a, QD / 4 + QB, Tin, C, gen)) return;
+                stamp(l, TS_O_IN);
+                if (n_own > 0) {
+                    const ActQ A = xw_block<WT>(xw, QB, lane);
+                    float res[RMAX];
+                    if (!dot_batch(std::integral_constant<int, RMAX>{}, lb + g.offo, g.uo,
+                                   stream_row_units(WT, QD) - QD / 256, 0, n_own, QB, A, res))
+                        return fail();
+#pragma unroll
+                    for (int r = 0; r < RMAX; r++) {
+                        const int row = g.row0o + cw + NCW * r;
+                        if (r < n_own && row < D) {
+                            h_own[r] += res[r];  // elementwise_add (layers.rs:81-109)
+                            if (lane == 0) putf(X.h + row, h_own[r], T);
+                        }
+                    }
+                }
             }
-            {
-                int rr[8];
-                gu_rows(wg, rr);
-                const MatView mv = view_of(LY[l].gateup);
-                load_rows(Wg, mv, rr, lane);
-            }
+            consumed(lb + g.offg);
             stamp(l, TS_O);
         }
 
         // ------------------------------------------------ gate/up + SiLU*up + quant
         {
             const unsigned T = tag(l, PH_GU);
-            const bool work = wg < gu_tiles;
-            if (work) {
-                load_gains(nw, LY[l].ffn_norm, D);
-                if (!gather(S, X.h, D, tag(l, PH_O), C)) return;
-                x_from_xw(x, S, D);
-            }
-            stamp(l, TS_GU_IN);
-            if (work) {
-                norm_quant<WT>(S, x, nw, D, a.eps, nullptr, nullptr, nullptr);
-                Act<1> A;
-                act_from_lds<WT>(A, S, KB, lane);
-                float res[8];
-                dot_rows<WT, 1, 8>(Wg, A, KB, lane, res);
-                if (lane == 0) {
+            if (g.ng > 0) {
+                const Gains gn = load_gains(LY[l].ffn_norm, D);
+                const long long rw0 = ring_wait;
+                if (!norm_quant(S, X.h, tag(l, PH_O), embed_at, gn, D, a.eps, nullptr, nullptr, nullptr, gen, C))
+                    return;
+                stamp(l, TS_GU_IN);
+                const ActQ A = act_lane(S, D);
+                stamp(l, TS_GU_NORM);
+                const int pu = stream_row_units(WT, D) - D / 256;
+                // rows i = cw + NCW r < 64, four per batch
+                const int ng_w = (64 - cw + NCW - 1) / NCW;
+#pragma unroll 1
+                for (int r0 = 0; r0 < ng_w; r0 += 4) {
+                    const int n = min(4, ng_w - r0);
+                    float res[4];
+                    if (!dot_batch(std::integral_constant<int, 4>{}, lb + g.offg, g.ua, pu, r0, n, KB, A, res))
+                        return fail();
+                    consumed(lb + g.offg + (cw + NCW * (r0 + n - 1) + 1) * g.ua);
+                    if (lane == 0) {
 #pragma unroll
-                    for (int r = 0; r < 8; r++) S.gu[wave * 8 + r] = res[r];
+                        for (int r = 0; r < 4; r++)
+                            if (r < n) S.gu[cw + NCW * (r0 + r)] = res[r];
+                    }
                 }
-            }
-            stamp(l, TS_GU_DOT);
-            if (work) {
-                __syncthreads();
-                if (wave == 0) {
+                stamp(l, TS_GU_DOT);
+                put_duration(l, TS_RING_GU, ring_wait - rw0);
+                if (!csync(S, gen, C)) return;
+                if (cw == 0) {
                     // layers::ffn (layers.rs:64-77): silu(gate) * up, then the
                     // down projection's Q8_0 quantization per 32-block.
                     const int j = lane & 31;
                     const float gt = S.gu[j];
                     const float up = S.gu[32 + j];
                     const float f = (gt * sq_sigmoid(gt)) * up;
-                    quant_put(f, lane, wg, X.f, X.f + F / 4, T, lane < 32);
+                    quant_put(f, lane, g.tile, X.f, X.f + F / 4, T, lane < 32);
                 }
             }
-            {
-                const int rr[1] = {gw < D ? gw : -1};
-                const MatView mv = view_of(LY[l].down);
-                load_rows(Wd, mv, rr, lane);
-            }
+            consumed(lb + g.offd);
             stamp(l, TS_GU);
         }
 
         // ------------------------------------------------ down + residual
         {
             const unsigned T = tag(l, PH_DOWN);
-            const bool work = wg * SW < D;
             const int FB = F >> 5;
-            if (work && !gather(S, X.f, F / 4 + FB, tag(l, PH_GU), C)) return;
-            stamp(l, TS_DOWN_IN);
-            if (work && gw < D) {
-                h_own += dot_row_xw<WT, 4>(Wd, S, FB, lane);
-                if (lane == 0) putf(X.h + gw, h_own, T);
+            if (g.row0o < D) {
+                // A workgroup without a gate/up tile passed no barrier since
+                // its o rows read xw: one here keeps the gather from
+                // overwriting it early.
+                if (g.ng == 0 && !csync(S, gen, C)) return;
+                unsigned* xw = next_xw();
+                if (!gather(S, xw, X.f, F / 4 + FB, tag(l, PH_GU), C, gen)) return;
+                stamp(l, TS_DOWN_IN);
+                if (n_own > 0) {
+                    const int pu = stream_row_units(WT, F) - F / 256;
+                    if (!ensure(lb + g.offd + (cw + NCW * (n_own - 1) + 1) * g.ud)) return fail();
+                    // lane blocks b = lane + 64 k (k < FMAX / 2048), activations
+                    // read once for both rows
+                    // lane blocks b = lane + 64 k (k < nk), both rows' reads
+                    // issued before any arithmetic
+                    constexpr int KD = FMAX / 2048;
+                    const int nk = (FB + 63) / 64;
+                    unsigned rb[RMAX];
+#pragma unroll
+                    for (int r = 0; r < RMAX; r++) rb[r] = ring_pos(lb + g.offd + (cw + NCW * (r < n_own ? r : 0)) * g.ud);
+                    ActQ Ak[KD];
+#pragma unroll
+                    for (int k = 0; k < KD; k++) {
+                        if (k >= nk) break;
+                        const int b = lane + 64 * k;
+                        Ak[k] = xw_block<WT>(xw, FB, b < FB ? b : 0);
+                    }
+                    float t[RMAX] = {0.0f, 0.0f};
+#pragma unroll
+                    for (int r = 0; r < RMAX; r++) {
+                        if (r >= n_own) break;
+                        RowData rd[KD];
+#pragma unroll
+                        for (int k = 0; k < KD; k++) {
+                            if (k >= nk) break;
+                            const int b = lane + 64 * k;
+                            rd[k] = row_fetch<WT>(S, rb[r], pu, b < FB ? b : 0);
+                        }
+#pragma unroll
+                        for (int k = 0; k < KD; k++) {
+                            if (k >= nk) break;
+                            t[r] += row_math<WT>(rd[k], Ak[k], lane + 64 * k < FB);
+                        }
+                    }
+                    wave_totals(t);
+#pragma unroll
+                    for (int r = 0; r < RMAX; r++) {
+                        if (r >= n_own) continue;
+                        const float res = t[r];
+                        const int row = g.row0o + cw + NCW * r;
+                        if (row < D) {
+                            h_own[r] += res;
+                            if (lane == 0) putf(X.h + row, h_own[r], T);
+                        }
+                    }
+                }
             }
-            if (l + 1 < a.n_layers) {
-                int rr[2];
-                qkv_rows(gw, rr);
-                const MatView mn = view_of(LY[l + 1].qkv);
-                load_rows(Wq, mn, rr, lane);
-            }
+            consumed(lb + g.LU);
             stamp(l, TS_DOWN);
+            put_duration(l, TS_RING_ALL, ring_wait);
+            ring_wait = 0;
         }
     }
 
     // ---------------------------------------------------- final norm + LM head
     {
-        const int units = (a.vocab + 3) / 4;
-        {
-            int rr[4];
-            head_rows(gw, rr);
-            load_rows(Wh0, a.head, rr, lane);
-        }
-        load_gains(nw, a.out_norm, D);
-        if (!gather(S, X.h, D, tag(a.n_layers - 1, PH_DOWN), C)) return;
-        x_from_xw(x, S, D);
-        stamp(a.n_layers, 0);
+        const Gains gn = load_gains(a.out_norm, D);
         const bool dbg = wg == 0 && a.last_hidden != nullptr;
-        norm_quant<WT>(S, x, nw, D, a.eps, dbg ? a.last_hidden : nullptr, a.head_qs, a.head_d);
-        Act<1> A;
-        act_from_lds<WT>(A, S, KB, lane);
+        if (!norm_quant(S, X.h, tag(a.n_layers - 1, PH_DOWN), embed_at, gn, D, a.eps, dbg ? a.last_hidden : nullptr,
+                        a.head_qs, a.head_d, gen, C))
+            return;
+        stamp(a.n_layers, 0);
+        const ActQ A = act_lane(S, D);
+        const int pu = stream_row_units(WT, D) - D / 256;
+        const int hb = a.n_layers * g.LU;
+        const int nh_w = g.nh > cw ? (g.nh - cw + NCW - 1) / NCW : 0;  // rows of this wavefront
+        // Lane r (< 4) of each batch takes the batch's row r: it stores that
+        // logit and keeps a running (value, index, last NaN) over its rows;
+        // the lanes merge once after the loop.
         float best_v = -INFINITY;
         int best_i = -1, nan_i = -1;
-        auto compute = [&](const Rows<WT, 1, 4>& Wb, int uu) {
+#pragma unroll 1
+        for (int r0 = 0; r0 < nh_w; r0 += 4) {
+            const int n = min(4, nh_w - r0);
             float res[4];
-            dot_rows<WT, 1, 4>(Wb, A, KB, lane, res);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = 4 * uu + r;
-                if (row >= a.vocab) continue;
-                if (lane == r) st_c(&a.logits[row], res[r]);
-                const float v = res[r];
-                if (v != v) {
-                    nan_i = row > nan_i ? row : nan_i;
-                } else if (v > best_v || (v == best_v && row > best_i)) {
+            if (!dot_batch(std::integral_constant<int, 4>{}, hb, g.ua, pu, r0, n, KB, A, res)) return fail();
+            consumed(hb + (cw + NCW * (r0 + n - 1) + 1) * g.ua);
+            const float v = lane == 0 ? res[0] : (lane == 1 ? res[1] : (lane == 2 ? res[2] : res[3]));
+            const int row = g.row0h + cw + NCW * (r0 + lane);
+            if (lane < n && row < a.vocab) {
+                st_c(&a.logits[row], v);
+                if (v != v) nan_i = row;  // rows grow along the loop
+                else if (v > best_v || (v == best_v && row > best_i)) {
                     best_v = v;
                     best_i = row;
                 }
             }
-        };
-        int u = gw;
-        while (u < units) {
-            if (u + NW < units) {
-                int rr[4];
-                head_rows(u + NW, rr);
-                load_rows(Wh1, a.head, rr, lane);
-            }
-            compute(Wh0, u);
-            u += NW;
-            if (u >= units) break;
-            if (u + NW < units) {
-                int rr[4];
-                head_rows(u + NW, rr);
-                load_rows(Wh0, a.head, rr, lane);
-            }
-            compute(Wh1, u);
-            u += NW;
         }
-        block_arg(S, best_v, best_i, nan_i);
+        wave_arg(best_v, best_i, nan_i);
+        consumed(g.total);
         // The logits must be visible before the partial is (the NaN rule may
-        // rescan them): wait for this workgroup's stores, then publish.
+        // rescan them): wait for this wavefront's stores, then publish.
         __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        if (lane == 0) {
+            S.bv[cw] = best_v;
+            S.bi[cw] = best_i;
+            S.bn[cw] = nan_i;
+        }
+        if (!csync(S, gen, C)) return;
         if (tid == 0) {
-            putf(X.p + 3 * wg, best_v, head_tag);
-            put(X.p + 3 * wg + 1, (unsigned)best_i, head_tag);
-            put(X.p + 3 * wg + 2, (unsigned)nan_i, head_tag);
+            float bv = S.bv[0];
+            int bi = S.bi[0], bn = S.bn[0];
+            for (int w = 1; w < NCW; w++) arg_merge(bv, bi, bn, S.bv[w], S.bi[w], S.bn[w]);
+            putf(X.p + 3 * wg, bv, head_tag);
+            put(X.p + 3 * wg + 1, (unsigned)bi, head_tag);
+            put(X.p + 3 * wg + 2, (unsigned)bn, head_tag);
         }
         stamp(a.n_layers, 1);
     }
 
     // ---------------------------------------------------- greedy (workgroup 0)
     if (wg != 0) return;
-    if (!gather(S, X.p, 3 * G, head_tag, C)) return;
     {
+        unsigned* xw = next_xw();
+        if (!gather(S, xw, X.p, 3 * G, head_tag, C, gen)) return;
         float bv = -INFINITY;
         int bi = -1, bn = -1;
-        for (int k = tid; k < G; k += SNT)
-            arg_merge(bv, bi, bn, __builtin_bit_cast(float, S.xw[3 * k]), (int)S.xw[3 * k + 1], (int)S.xw[3 * k + 2]);
-        block_arg(S, bv, bi, bn);
+        for (int k = tid; k < G; k += CNT)
+            arg_merge(bv, bi, bn, __builtin_bit_cast(float, xw[3 * k]), (int)xw[3 * k + 1], (int)xw[3 * k + 2]);
+        wave_arg(bv, bi, bn);
+        if (lane == 0) {
+            S.bv[cw] = bv;
+            S.bi[cw] = bi;
+            S.bn[cw] = bn;
+        }
+        if (!csync(S, gen, C)) return;
+        bv = S.bv[0];
+        bi = S.bi[0];
+        bn = S.bn[0];
+        for (int w = 1; w < NCW; w++) arg_merge(bv, bi, bn, S.bv[w], S.bi[w], S.bn[w]);
         int result = bi;
         if (bn >= 0) {
             // Iterator::max_by hands the lead to the later element whenever a
@@ -908,11 +1311,22 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
             // that NaN when nothing follows it.
             float cv = -INFINITY;
             int ci = -1, cn = -1;
-            for (int i = bn + 1 + tid; i < a.vocab; i += SNT) {
+            for (int i = bn + 1 + tid; i < a.vocab; i += CNT) {
                 const float v = ld_c(&a.logits[i]);
                 if (v == v) arg_merge(cv, ci, cn, v, i, -1);
             }
-            block_arg(S, cv, ci, cn);
+            wave_arg(cv, ci, cn);
+            if (!csync(S, gen, C)) return;  // every wavefront has read S.bv
+            if (lane == 0) {
+                S.bv[cw] = cv;
+                S.bi[cw] = ci;
+                S.bn[cw] = cn;
+            }
+            if (!csync(S, gen, C)) return;
+            cv = S.bv[0];
+            ci = S.bi[0];
+            cn = S.bn[0];
+            for (int w = 1; w < NCW; w++) arg_merge(cv, ci, cn, S.bv[w], S.bi[w], S.bn[w]);
             result = ci >= 0 ? ci : bn;
         }
         if (tid == 0) {
@@ -930,28 +1344,111 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     }
 }
 
+// Copies the weight rows into the per-CU streams: blockIdx.y is the CU,
+// unit u = blockIdx.x * 256 + threadIdx.x of its stream.
+template <int WT>
+__global__ __launch_bounds__(256) void build_stream_kernel(StepArgs a, uint8_t* dst) {
+    const int G = gridDim.y, wg = blockIdx.y;
+    const int D = a.dim, F = a.ffn;
+    const int QD = a.n_heads * HDIM, KVD = a.n_kv_heads * HDIM;
+    const StreamGeo g = stream_geo(WT, a.n_layers, D, F, QD, KVD, a.vocab, G, wg);
+    const int u = blockIdx.x * 256 + threadIdx.x;
+    if (u >= g.total) return;
+    MatView m;
+    int row, ur;
+    if (u >= a.n_layers * g.LU) {
+        const int r = u - a.n_layers * g.LU;
+        m = a.head;
+        row = g.row0h + r / g.ua;
+        ur = r % g.ua;
+        if (row >= a.vocab) row = 0;
+    } else {
+        const int l = u / g.LU, r = u % g.LU;
+        const StepLayer& Ly = a.layers[l];
+        if (r < g.offo) {
+            m = Ly.qkv;
+            row = g.row0q + r / g.ua;
+            ur = r % g.ua;
+            if (row >= QD + 2 * KVD) row = 0;
+        } else if (r < g.offg) {
+            m = Ly.o;
+            row = g.row0o + (r - g.offo) / g.uo;
+            ur = (r - g.offo) % g.uo;
+            if (row >= D) row = 0;
+        } else if (r < g.offd) {
+            const int i = (r - g.offg) / g.ua;
+            m = Ly.gateup;
+            row = i < 32 ? g.tile * 32 + i : F + g.tile * 32 + (i - 32);
+            ur = (r - g.offg) % g.ua;
+        } else {
+            m = Ly.down;
+            row = g.row0o + (r - g.offd) / g.ud;
+            ur = (r - g.offd) % g.ud;
+            if (row >= D) row = 0;
+        }
+    }
+    const int pu = stream_row_units(WT, m.k) - m.k / 256;  // payload units of a row
+    const uint8_t* src = ur < pu ? (const uint8_t*)m.qs + (size_t)row * pu * 16 + (size_t)ur * 16
+                                 : (const uint8_t*)m.scale + (size_t)row * (m.k / 16) + (size_t)(ur - pu) * 16;
+    *(uint4*)(dst + ((size_t)wg * a.stream_stride + u) * 16) = *(const uint4*)src;
+}
+
 }  // namespace
 
+// A batch of R rows per wavefront, rows dealt round-robin over NCW
+// wavefronts: the batch awaited by the wavefront with the lowest next row ends
+// at most min(NCW * R, rows of the phase) rows past the consumed boundary.
+static bool ring_fits(int dim, int ffn, int n_heads, int n_kv_heads, int grid) {
+    const int QD = n_heads * HDIM, KVD = n_kv_heads * HDIM;
+    const int pairs = ((QD + 2 * KVD) / 2 + grid - 1) / grid;  // QKV row pairs per CU
+    const int no = (dim + grid - 1) / grid;                     // o / down rows per CU
+    auto span = [](int rows, int R, int units) { return (int64_t)std::min(NCW * R, rows) * units + 64 <= RU; };
+    const int ua = stream_row_units(WT_Q8_0, dim);
+    return span(pairs, 2, 2 * ua) && span(64, 4, ua) && span(1 << 30, 4, ua) &&
+           span(no, RMAX, stream_row_units(WT_Q8_0, QD)) && span(no, RMAX, stream_row_units(WT_Q8_0, ffn));
+}
+
 bool decode_step_fits(int dim, int ffn, int n_heads, int n_kv_heads, int grid) {
-    // every phase but the LM head gives each wavefront at most one unit:
-    // QKV row pairs and o/down rows per wavefront, gate/up tiles per workgroup
-    const int nw = grid * SW;
-    const int q_units = (n_heads + n_kv_heads * 2) * HDIM / 2;
-    return dim <= DMAX && ffn <= FMAX && dim % 32 == 0 && ffn % 32 == 0 && n_heads * HDIM <= DMAX &&
-           n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= MAXG && q_units <= nw &&
-           dim <= nw && ffn / 32 <= grid && 3 * grid <= XMAX;
+    // Each CU owns at most NCW * RMAX o/down rows (its residual rows) and one
+    // gate/up tile; the K widths are multiples of 256, so every row is a whole
+    // number of 16-byte units (payload and scales).
+    const int QD = n_heads * HDIM;
+    return grid > 0 && dim <= DMAX && ffn <= FMAX && dim % 256 == 0 && ffn % 256 == 0 && QD % 256 == 0 &&
+           QD <= DMAX && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= MAXG &&
+           (dim + grid - 1) / grid <= NCW * RMAX && ffn / 32 <= grid && 3 * grid <= XMAX &&
+           (n_heads + 2 * n_kv_heads) * HDIM / 2 <= 2 * NCW * grid && ring_fits(dim, ffn, n_heads, n_kv_heads, grid);
+}
+
+size_t decode_stream_stride(int wtype, int n_layers, int dim, int ffn, int n_heads, int n_kv_heads, int vocab,
+                            int grid) {
+    const StreamGeo g = stream_geo(wtype, n_layers, dim, ffn, n_heads * HDIM, n_kv_heads * HDIM, vocab, grid, 0);
+    return ((size_t)g.total + 63) / 64 * 64;
+}
+
+int launch_build_stream(hipStream_t s, int wtype, const StepArgs& a, int grid, void* dst) {
+    if (wtype != WT_Q8_0 && wtype != WT_Q4_0)
+        return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: Q8_0 and Q4_0 weights only");
+    if (!decode_step_fits(a.dim, a.ffn, a.n_heads, a.n_kv_heads, grid))
+        return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: shape not supported");
+    const size_t stride = decode_stream_stride(wtype, a.n_layers, a.dim, a.ffn, a.n_heads, a.n_kv_heads, a.vocab, grid);
+    if (a.stream_stride != stride) return set_error(SQ_ERR_ARG, "weight stream: stride does not match the model");
+    const dim3 bl((unsigned)((stride + 255) / 256), (unsigned)grid);
+    if (wtype == WT_Q8_0)
+        hipLaunchKernelGGL(build_stream_kernel<WT_Q8_0>, bl, dim3(256), 0, s, a, (uint8_t*)dst);
+    else
+        hipLaunchKernelGGL(build_stream_kernel<WT_Q4_0>, bl, dim3(256), 0, s, a, (uint8_t*)dst);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("weight stream build: ") + hipGetErrorString(e));
+    return 0;
 }
 
 int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid) {
-    if (a.dim > DMAX || a.dim % 32 != 0 || a.ffn % 32 != 0 || a.ffn > FMAX)
-        return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: dim <= 2048, ffn <= 8192, multiples of 32");
-    if (a.n_kv_heads <= 0 || a.n_heads % a.n_kv_heads != 0 || a.n_heads / a.n_kv_heads > MAXG)
-        return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: GQA group size must be at most 8");
-    if (a.n_heads * HDIM > DMAX)
-        return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: q width must be at most 2048");
     if (!decode_step_fits(a.dim, a.ffn, a.n_heads, a.n_kv_heads, grid))
-        return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: the grid is too small for one unit per "
-                                             "wavefront in every phase");
+        return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: shape not supported (dim <= 2048, ffn <= 8192, "
+                                             "multiples of 256, GQA group <= 4)");
+    if (a.stream == nullptr ||
+        a.stream_stride != decode_stream_stride(wtype, a.n_layers, a.dim, a.ffn, a.n_heads, a.n_kv_heads, a.vocab, grid))
+        return set_error(SQ_ERR_ARG, "persistent decode step: the weight stream was not built for this grid");
     // One workgroup per CU (the grid is the CU count and a CU holds one of
     // these workgroups), so every workgroup is resident at once; were one
     // not, the bounded waits would end the step with an error, not a hang.

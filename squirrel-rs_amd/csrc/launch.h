@@ -150,6 +150,10 @@ size_t exchange_words(int dim, int ffn, int n_heads, int n_kv_heads, int max_til
 // ticks, after which every workgroup leaves.
 struct StepArgs {
     const StepLayer* layers;  // device array [n_layers]
+    // The weight rows in the order each CU multiplies them (launch_build_stream):
+    // CU w's stream starts at unit w * stream_stride (16-byte units).
+    const void* stream;
+    size_t stream_stride;
     MatView embd, head;
     const float* out_norm;
     int n_layers, dim, ffn, n_heads, n_kv_heads, vocab;
@@ -175,13 +179,19 @@ struct StepArgs {
     int8_t* head_qs;
     uint16_t* head_d;
     // Optional timeline (measurement): per workgroup, trace_stride wall-clock
-    // stamps, 16 slots per layer (k_step.hip TraceSlot) after slot 0 (start).
+    // stamps, 20 slots per layer (k_step.hip TraceSlot) after slot 0 (start).
     unsigned long long* trace;
     int trace_stride;
 };
 
 // True when the step kernel can run the model with `grid` workgroups.
 bool decode_step_fits(int dim, int ffn, int n_heads, int n_kv_heads, int grid);
+// 16-byte units per CU in the weight stream of a model run over `grid` CUs.
+size_t decode_stream_stride(int wtype, int n_layers, int dim, int ffn, int n_heads, int n_kv_heads, int vocab,
+                            int grid);
+// Fills dst (grid * stride units) with the per-CU weight streams of the
+// layers, head and geometry in `a` (a.stream_stride must be the stride).
+int launch_build_stream(hipStream_t s, int wtype, const StepArgs& a, int grid, void* dst);
 // Launch of one decode step over `grid` workgroups (one per CU).
 int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid);
 // Workgroups for the decode step on the current device (one per CU).

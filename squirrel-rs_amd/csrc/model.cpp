@@ -699,6 +699,11 @@ int setup_persistent(sq_ctx* c) {
     a.head_d = c->head_d;
     a.trace = nullptr;
     a.trace_stride = 0;
+    a.stream_stride = decode_stream_stride(m->wtype, g.n_layers, g.dim, g.ffn, g.n_heads, g.n_kv_heads, g.vocab, grid);
+    if ((st = dmalloc(&c->s_stream, a.stream_stride * 16 * (size_t)grid))) return st;
+    a.stream = c->s_stream;
+    if ((st = launch_build_stream(c->stream, m->wtype, a, grid, c->s_stream))) return st;
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
     c->step_grid = grid;
     c->persist = true;
     return 0;
@@ -806,7 +811,7 @@ void ctx_destroy(sq_ctx* c) {
     dfree(c->dbg_qs); dfree(c->dbg_d); dfree(c->last_hidden); dfree(c->head_qs); dfree(c->head_d);
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
     dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad);
-    dfree(c->d_layers); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
+    dfree(c->d_layers); dfree(c->s_stream); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
     if (c->h_pinned) (void)hipHostFree(c->h_pinned);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;

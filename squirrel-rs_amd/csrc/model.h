@@ -114,6 +114,7 @@ struct sq_ctx {
     int step_grid = 0;
     sq::StepArgs step{};
     sq::StepLayer* d_layers = nullptr;
+    uint8_t* s_stream = nullptr;  // per-CU weight streams
     unsigned long long* s_xchg = nullptr;  // exchange words
     unsigned* s_epoch = nullptr;
     int* s_error = nullptr;
