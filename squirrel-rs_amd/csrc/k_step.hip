@@ -1008,9 +1008,6 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 }
                 const float v = (s0 + lane < P) ? dot * scale : -INFINITY;
                 if (it == wg) stamp(l, TS_ATT_S);
-                const float m = wave_maximum(v);
-                const float pr = (v == -INFINITY) ? 0.0f : expf(v - m);
-                const float sum = wave_total(pr);
                 // V column `lane` of the tile (issued once the scores are done:
                 // with the K row also live it would not fit in registers)
                 float vv[TPOS];
@@ -1020,13 +1017,18 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                     const gptr<const float> vrow = vc + (size_t)(s0 + sp < pos ? s0 + sp : 0) * KVD + gh * HDIM;
                     vv[sp] = vrow[lane];
                 }
-                // o[lane] = sum over positions of p * v (lane = dimension)
+                const float m = wave_maximum(v);
+                const float pr = (v == -INFINITY) ? 0.0f : expf(v - m);
+                const float sum = wave_total(pr);
+                // o[lane] = sum over positions of p * v (lane = dimension), in
+                // position order.  Positions past pos weigh 0 (their vv is a
+                // finite stand-in); the new row, the last position, is added
+                // last from its exchange word.
+                const float pm = s0 + lane == pos ? 0.0f : pr;
                 float o = 0.0f;
 #pragma unroll
-                for (int sp = 0; sp < TPOS; sp++) {
-                    const float vs = s0 + sp < pos ? vv[sp] : (s0 + sp == pos ? vn : 0.0f);
-                    o += lane_value(pr, sp) * vs;
-                }
+                for (int sp = 0; sp < TPOS; sp++) o += lane_value(pm, sp) * vv[sp];
+                if (cur) o += lane_value(pr, pos - s0) * vn;
                 if (ntiles == 1) {
                     quant_put(o / sum, lane, h * 2, X.a, X.a + QD / 4, T, true);
                 } else {
