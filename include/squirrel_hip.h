@@ -120,7 +120,10 @@ void sq_ctx_free(sq_ctx* c);
 int sq_ctx_reset(sq_ctx* c);
 /* How decode steps run: 1 = the persistent one-launch-per-token kernel
  * (Q8_0 / Q4_0 integer path, head_dim 64, width <= 2048), 0 = one kernel per
- * op replayed as a hipGraph.  No reference counterpart (measurement aid). */
+ * op replayed as a hipGraph.  No reference counterpart (measurement aid).
+ * The persistent kernel occupies one workgroup per CU; the environment
+ * variable SQUIRREL_STEP_GRID, read by sq_ctx_new, caps that count (a cap the
+ * shape does not fit in selects the multi-kernel path). */
 int sq_ctx_decode_kernel(const sq_ctx* c);
 /* Timeline of the persistent decode step (measurement aid, no reference
  * counterpart).  With tracing enabled every step records, per workgroup,
@@ -131,8 +134,8 @@ int sq_ctx_decode_kernel(const sq_ctx* c);
  * quantized, 7 gate/up dot done, 8 gate/up done, 9 down inputs gathered,
  * 10 down done, 11-13 the first attention item's q gathered / scores /
  * outputs published, 14-15 durations (ticks) the first compute wavefront
- * waited for weights in the gate/up phase / the layer, 16-17 the activation
- * read back after slots 0 / 6; then [1 + 20L] LM-head inputs gathered,
+ * waited for weights in the gate/up phase / the layer, 16 the QKV input
+ * row's polls begin; then [1 + 20L] LM-head inputs gathered,
  * [2 + 20L] LM head done, [3 + 20L] token resolved (workgroup 0 only); 0 where
  * a slot was not reached.
  * _read copies the most recent step's stamps (grid * stride values); with

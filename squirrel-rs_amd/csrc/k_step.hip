@@ -257,6 +257,38 @@ __device__ __forceinline__ bool await_words(const u64* const (&p)[N], u64 (&w)[N
     }
 }
 
+// await_words with the addresses formed by addr(j) (null: no word) at each
+// use instead of held in registers.
+template <int N, typename A>
+__device__ __forceinline__ bool await_words_at(A&& addr, u64 (&w)[N], unsigned tag, const Ctl& C, const int* abort) {
+    auto pending = [&]() {
+        bool any = false;
+#pragma unroll
+        for (int j = 0; j < N; j++) any |= addr(j) != nullptr && (unsigned)(w[j] >> 32) != tag;
+        return any;
+    };
+    if (!pending()) return true;
+    long long t0 = 0;  // read at the first periodic check (see await_words)
+    for (int polls = 1;; polls++) {
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int j = 0; j < N; j++) {
+            const u64* p = addr(j);
+            if (p != nullptr && (unsigned)(w[j] >> 32) != tag) w[j] = ld_c(p);
+        }
+        if (!pending()) return true;
+        if ((polls & 15) == 0) {
+            if (ld_c(C.error) != 0 || lds_ld(abort)) return false;
+            const long long now = wall_clock64();
+            if (polls == 16) t0 = now;
+            if (now - t0 > C.limit || polls > (1 << 20)) {
+                st_c(C.error, 1);
+                return false;
+            }
+        }
+    }
+}
+
 // Spin until an LDS condition holds (bounded), then acquire.  False: abandon
 // the launch.
 template <typename F>
@@ -739,8 +771,7 @@ enum TraceSlot : int {
     TS_ATT_PV = 13,    // attention: outputs published (first item)
     TS_RING_GU = 14,   // ticks wavefront 0 waited on the ring in the gate/up phase (a duration)
     TS_RING_ALL = 15,  // ticks wavefront 0 waited on the ring in the layer (a duration)
-    TS_QKV_NORM = 16,  // QKV: quantized activation read back
-    TS_GU_NORM = 17,   // gate/up: quantized activation read back
+    TS_QKV_POLL = 16,  // QKV: the input row's polls begin
     TS_PER_LAYER = 20
 };
 
@@ -781,6 +812,11 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     const uint32_t tok = *a.token;
     const int P = pos + 1;
     const int ntiles = (P + TPOS - 1) / TPOS;
+    // Attention work: chunks of tpc consecutive 64-position tiles per KV
+    // head, as few tiles per chunk as lets one round of the grid take every
+    // (KV head, chunk) item; more than one chunk per head adds a merge phase.
+    const int tpc = (ntiles * a.n_kv_heads + G - 1) / G;
+    const int nchunks = (ntiles + tpc - 1) / tpc;
     const Xchg X = a.x;
     const cptr<StepLayer> LY = (cptr<StepLayer>)a.layers;
     int gen = 0;  // compute-group barrier count
@@ -894,12 +930,12 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 }
                 const Gains gn = load_gains(LY[l].attn_norm, D);
                 const bool dbg = l == 0 && wg == 0 && a.dbg_normed != nullptr;
+                stamp(l, TS_QKV_POLL);
                 if (!norm_quant(S, l == 0 ? nullptr : X.h, l == 0 ? 0u : tag(l - 1, PH_DOWN), embed_at, gn, D, a.eps,
                                 dbg ? a.dbg_normed : nullptr, a.dbg_qs, a.dbg_d, gen, C))
                     return;
                 stamp(l, TS_QKV_IN);
                 const ActQ A = act_lane(S, D);
-                stamp(l, TS_QKV_NORM);
                 const int pu = stream_row_units(WT, D) - D / 256;
                 if (np > 0) {
                     // a pair is two consecutive rows: 2 * ua units
@@ -951,33 +987,38 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
         }
 
         // ------------------------------------------------ attention (GQA)
-        // Work item = (kv head, 64-position tile).  Wavefront cw < GQ takes
-        // query head gh*GQ + cw on its own: lane = position for the scores
-        // (its K row in registers, q[d] read from lane d), lane = dimension
-        // for the output (its V column in registers, p read from lane
-        // `position`).  Cached rows (positions < pos) come from the KV cache,
-        // the new rows from this launch's exchange words; the new K row
-        // reaches its lane through a 64-word scratch of the wavefront in xw.
+        // Work item = (kv head, chunk of tpc 64-position tiles).  Wavefront
+        // cw < GQ takes query head gh*GQ + cw on its own and walks the
+        // chunk's tiles with an online softmax (the tile-merge arithmetic of
+        // the merge phase): lane = position for the scores (its K row in
+        // registers, q[d] read from lane d), lane = dimension for the output
+        // (its V column in registers, p read from lane `position`).  Cached
+        // rows (positions < pos) come from the KV cache, the new rows from this
+        // launch's exchange words; the new K row reaches its lane through a
+        // 64-word scratch of the wavefront in xw.
         {
             const unsigned Tin = tag(l, PH_QKV), T = tag(l, PH_ATTN);
-            const int items = a.n_kv_heads * ntiles;
+            const int items = a.n_kv_heads * nchunks;
             const float scale = 1.0f / sqrtf((float)HDIM);
             for (int it = wg; it < items; it += G) {
-                const int gh = it / ntiles, tile = it % ntiles;
-                const int s0 = tile * TPOS;
-                const bool cur = s0 + TPOS > pos;  // this tile holds the new position
+                const int gh = it / nchunks, chunk = it % nchunks;
+                const int t_begin = chunk * tpc, t_end = min(ntiles, t_begin + tpc);
+                const bool cur = t_end == ntiles;  // this chunk holds the new position
                 if (cw >= GQ) continue;
                 const int h = gh * GQ + cw;
-                // K row of position s0 + lane and V column `lane` of the tile
-                // (row 0 stands in for positions without a cached row; their
-                // scores are masked and their V values replaced below)
-                const bool cached = s0 + lane < pos;
-                const gptr<const sq_v4f> kp =
-                    (gptr<const sq_v4f>)(kc + (size_t)(cached ? s0 + lane : 0) * KVD + gh * HDIM);
-                sq_v4f kr[HDIM / 4];
+                // the first tile's K rows are requested before the q words are
+                // polled (and stay ahead of the polling loop)
+                auto load_k = [&](int s0, sq_v4f (&kr)[HDIM / 4]) {
+                    const bool cached = s0 + lane < pos;
+                    const gptr<const sq_v4f> kp =
+                        (gptr<const sq_v4f>)(kc + (size_t)(cached ? s0 + lane : 0) * KVD + gh * HDIM);
 #pragma unroll
-                for (int i = 0; i < HDIM / 4; i++) kr[i] = kp[i];
-                // q[lane] of head h and, in the last tile, the new K/V rows' element lane
+                    for (int i = 0; i < HDIM / 4; i++) kr[i] = kp[i];
+                };
+                sq_v4f kr[HDIM / 4];
+                load_k(t_begin * TPOS, kr);
+                asm volatile("" ::: "memory");
+                // q[lane] of head h and, in the last chunk, the new K/V rows' element lane
                 int t = tid;
                 asm volatile("" : "+v"(t));
                 const int d = t & 63;
@@ -987,57 +1028,93 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
 #pragma unroll
                 for (int j = 0; j < 3; j++) w[j] = pw[j] ? ld_c(pw[j]) : 0;
                 if (!await_words(pw, w, Tin, C, &S.abort)) return fail();
+                const float qv = __builtin_bit_cast(float, (unsigned)w[0]);
                 const float vn = __builtin_bit_cast(float, (unsigned)w[2]);
                 unsigned* scr = S.xw + cw * HDIM;  // the new K row
                 scr[lane] = (unsigned)w[1];
                 __builtin_amdgcn_wave_barrier();
                 if (it == wg) stamp(l, TS_ATT_Q);
-                if (s0 + lane == pos) {
+                float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
+                // One tile: scores with lane = position, then the output with
+                // lane = dimension.  A tile that is not the chunk's last holds
+                // its V column in two halves of registers (the first requested
+                // before the softmax, the second once the first is used) and
+                // requests the next tile's K rows meanwhile; the last tile
+                // requests its whole V column once the scores are done.
+                auto do_tile = [&](int tile, auto last_c) {
+                    constexpr bool LAST = decltype(last_c)::value;
+                    const int s0 = tile * TPOS;
+                    if (s0 + lane == pos) {
 #pragma unroll
-                    for (int i = 0; i < HDIM / 4; i++) kr[i] = *(const sq_v4f*)(scr + 4 * i);
-                }
-                // scores = dot(q, k) * (1/sqrt(head_dim)) (attention.rs:52-55)
-                const float qv = __builtin_bit_cast(float, (unsigned)w[0]);
-                float dot = 0.0f;
+                        for (int i = 0; i < HDIM / 4; i++) kr[i] = *(const sq_v4f*)(scr + 4 * i);
+                    }
+                    // scores = dot(q, k) * (1/sqrt(head_dim)) (attention.rs:52-55)
+                    float dot = 0.0f;
 #pragma unroll
-                for (int i = 0; i < HDIM / 4; i++) {
-                    dot += lane_value(qv, 4 * i + 0) * kr[i].x;
-                    dot += lane_value(qv, 4 * i + 1) * kr[i].y;
-                    dot += lane_value(qv, 4 * i + 2) * kr[i].z;
-                    dot += lane_value(qv, 4 * i + 3) * kr[i].w;
-                }
-                const float v = (s0 + lane < P) ? dot * scale : -INFINITY;
-                if (it == wg) stamp(l, TS_ATT_S);
-                // V column `lane` of the tile (issued once the scores are done:
-                // with the K row also live it would not fit in registers)
-                float vv[TPOS];
+                    for (int i = 0; i < HDIM / 4; i++) {
+                        dot += lane_value(qv, 4 * i + 0) * kr[i].x;
+                        dot += lane_value(qv, 4 * i + 1) * kr[i].y;
+                        dot += lane_value(qv, 4 * i + 2) * kr[i].z;
+                        dot += lane_value(qv, 4 * i + 3) * kr[i].w;
+                    }
+                    const float v = (s0 + lane < P) ? dot * scale : -INFINITY;
+                    if (it == wg && tile == t_begin) stamp(l, TS_ATT_S);
+                    // V[s0 + sp][lane] for sp in [k0, k0 + n); row 0 stands in
+                    // for positions without a cached row (weight 0 below)
+                    auto load_v = [&](int k0, float* vv, auto n_c) {
 #pragma unroll
-                for (int sp = 0; sp < TPOS; sp++) {
-                    // row pointer uniform, lane offset in a register: scalar-base loads
-                    const gptr<const float> vrow = vc + (size_t)(s0 + sp < pos ? s0 + sp : 0) * KVD + gh * HDIM;
-                    vv[sp] = vrow[lane];
-                }
-                const float m = wave_maximum(v);
-                const float pr = (v == -INFINITY) ? 0.0f : expf(v - m);
-                const float sum = wave_total(pr);
-                // o[lane] = sum over positions of p * v (lane = dimension), in
-                // position order.  Positions past pos weigh 0 (their vv is a
-                // finite stand-in); the new row, the last position, is added
-                // last from its exchange word.
-                const float pm = s0 + lane == pos ? 0.0f : pr;
-                float o = 0.0f;
+                        for (int k = 0; k < decltype(n_c)::value; k++) {
+                            const int sp = k0 + k;
+                            // row pointer uniform, lane offset in a register: scalar-base loads
+                            const gptr<const float> vrow =
+                                vc + (size_t)(s0 + sp < pos ? s0 + sp : 0) * KVD + gh * HDIM;
+                            vv[k] = vrow[lane];
+                        }
+                    };
+                    constexpr int NV = LAST ? TPOS : TPOS / 2;
+                    float vv[NV];
+                    load_v(0, vv, std::integral_constant<int, NV>{});
+                    const float mt = wave_maximum(v);
+                    const float pr = (v == -INFINITY) ? 0.0f : expf(v - mt);
+                    const float lt = wave_total(pr);
+                    if (!LAST) load_k(s0 + TPOS, kr);
+                    // o[lane] = sum over positions of p * v (lane = dimension), in
+                    // position order.  Positions past pos weigh 0 (their V value
+                    // is a finite stand-in); the new row, the last position, is
+                    // added last from its exchange word.
+                    const float pm = s0 + lane == pos ? 0.0f : pr;
+                    float ot = 0.0f;
 #pragma unroll
-                for (int sp = 0; sp < TPOS; sp++) o += lane_value(pm, sp) * vv[sp];
-                if (cur) o += lane_value(pr, pos - s0) * vn;
-                if (ntiles == 1) {
-                    quant_put(o / sum, lane, h * 2, X.a, X.a + QD / 4, T, true);
+                    for (int k = 0; k < NV; k++) ot += lane_value(pm, k) * vv[k];
+                    if (!LAST) {
+                        asm volatile("" ::: "memory");  // the second half's loads stay after the first's use
+                        load_v(TPOS / 2, vv, std::integral_constant<int, NV>{});
+#pragma unroll
+                        for (int k = 0; k < NV; k++) ot += lane_value(pm, TPOS / 2 + k) * vv[k];
+                    }
+                    if (s0 + TPOS > pos) ot += lane_value(pr, pos - s0) * vn;
+                    // fold the tile into the chunk (the merge phase's arithmetic)
+                    if (mt != -INFINITY) {
+                        const float Mn = fmaxf(M, mt);
+                        const float es = (M == -INFINITY) ? 0.0f : expf(M - Mn);
+                        const float et = expf(mt - Mn);
+                        Lsum = Lsum * es + lt * et;
+                        O = O * es + ot * et;
+                        M = Mn;
+                    }
+                };
+#pragma unroll 1
+                for (int tile = t_begin; tile + 1 < t_end; tile++) do_tile(tile, std::false_type{});
+                do_tile(t_end - 1, std::true_type{});
+                if (nchunks == 1) {
+                    quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, T, true);
                 } else {
-                    // partial (o[64], m, l) of head h, tile `tile`
-                    u64* pt = X.t + ((size_t)h * a.max_tiles + tile) * (HDIM + 2);
-                    putf(pt + lane, o, T);
+                    // partial (o[64], m, l) of head h, chunk `chunk`
+                    u64* pt = X.t + ((size_t)h * a.max_tiles + chunk) * (HDIM + 2);
+                    putf(pt + lane, O, T);
                     if (lane == 0) {
-                        putf(pt + HDIM, m, T);
-                        putf(pt + HDIM + 1, sum, T);
+                        putf(pt + HDIM, M, T);
+                        putf(pt + HDIM + 1, Lsum, T);
                     }
                 }
                 if (it == wg) stamp(l, TS_ATT_PV);
@@ -1045,32 +1122,32 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
             // the scratch in xw is free again before the o gather writes xw
             if (wg < items && !csync(S, gen, C)) return;
             stamp(l, TS_ATTN);
-            if (ntiles > 1) {
-                // merge the tiles of each head, then quantize the row
+            if (nchunks > 1) {
+                // merge the chunks of each head, then quantize the row
                 const unsigned Tm = tag(l, PH_MERGE);
                 bool ok = true;
-                for (int h = wg * NCW + cw; h < a.n_heads && ok; h += G * NCW) {
+                // from the last workgroup down: those are the last to get attention items
+                for (int h = (G - 1 - wg) * NCW + cw; h < a.n_heads && ok; h += G * NCW) {
                     const int d = lane;
                     float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
-                    for (int t0 = 0; t0 < ntiles && ok; t0 += 2) {
-                        // (o[d], m, l) of tiles t0 and t0 + 1
-                        const u64* pw[6];
-                        u64 w[6];
+                    const u64* ph = X.t + (size_t)h * a.max_tiles * (HDIM + 2);
+                    // (o[d], m, l) of the chunks t0 .. t0 + MT - 1, polled as one
+                    // batch and merged in chunk order
+                    auto merge_batch = [&](int t0, auto mt_c) -> bool {
+                        constexpr int MT = decltype(mt_c)::value;
+                        auto addr = [&](int j) -> const u64* {
+                            const int tt = t0 + j / 3;
+                            if (tt >= nchunks) return nullptr;
+                            const u64* pt = ph + (size_t)tt * (HDIM + 2);
+                            return j % 3 == 0 ? pt + d : pt + HDIM + (j % 3 - 1);
+                        };
+                        u64 w[3 * MT];
 #pragma unroll
-                        for (int j2 = 0; j2 < 2; j2++) {
-                            const u64* pt = X.t + ((size_t)h * a.max_tiles + t0 + j2) * (HDIM + 2);
-                            const bool v = t0 + j2 < ntiles;
-                            pw[3 * j2 + 0] = v ? pt + d : nullptr;
-                            pw[3 * j2 + 1] = v ? pt + HDIM : nullptr;
-                            pw[3 * j2 + 2] = v ? pt + HDIM + 1 : nullptr;
-                        }
+                        for (int j = 0; j < 3 * MT; j++) w[j] = addr(j) ? ld_c(addr(j)) : 0;
+                        if (!await_words_at(addr, w, T, C, &S.abort)) return false;
 #pragma unroll
-                        for (int j = 0; j < 6; j++) w[j] = pw[j] ? ld_c(pw[j]) : 0;
-                        ok = await_words(pw, w, T, C, &S.abort);
-                        if (!ok) continue;
-#pragma unroll
-                        for (int j2 = 0; j2 < 2; j2++) {
-                            if (t0 + j2 >= ntiles) continue;
+                        for (int j2 = 0; j2 < MT; j2++) {
+                            if (t0 + j2 >= nchunks) continue;
                             const float mt = __builtin_bit_cast(float, (unsigned)w[3 * j2 + 1]);
                             if (mt == -INFINITY) continue;
                             const float Mn = fmaxf(M, mt);
@@ -1080,6 +1157,14 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                             O = O * es + __builtin_bit_cast(float, (unsigned)w[3 * j2]) * et;
                             M = Mn;
                         }
+                        return true;
+                    };
+                    // two chunks: one small batch; more: batches of eight
+                    if (nchunks <= 2) {
+                        ok = merge_batch(0, std::integral_constant<int, 2>{});
+                    } else {
+                        for (int t0 = 0; t0 < nchunks && ok; t0 += 8)
+                            ok = merge_batch(t0, std::integral_constant<int, 8>{});
                     }
                     // lanes of one wavefront agree on ok (any failure aborts)
                     if (__all(ok)) quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, Tm, true);
@@ -1092,7 +1177,7 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
 
         // ------------------------------------------------ o-projection + residual
         {
-            const unsigned Tin = tag(l, ntiles > 1 ? PH_MERGE : PH_ATTN), T = tag(l, PH_O);
+            const unsigned Tin = tag(l, nchunks > 1 ? PH_MERGE : PH_ATTN), T = tag(l, PH_O);
             const int QB = QD >> 5;
             if (g.row0o < D) {
                 unsigned* xw = next_xw();
@@ -1128,7 +1213,6 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                     return;
                 stamp(l, TS_GU_IN);
                 const ActQ A = act_lane(S, D);
-                stamp(l, TS_GU_NORM);
                 const int pu = stream_row_units(WT, D) - D / 256;
                 // rows i = cw + NCW r < 64, four per batch
                 const int ng_w = (64 - cw + NCW - 1) / NCW;

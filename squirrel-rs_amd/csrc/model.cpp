@@ -26,6 +26,7 @@
 #include <chrono>
 #include <memory>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <thread>
 
@@ -639,6 +640,13 @@ int setup_persistent(sq_ctx* c) {
         return 0;
     int grid = 0, st;
     if ((st = decode_step_max_grid(m->wtype, &grid))) return st;
+    // SQUIRREL_STEP_GRID caps the CUs the kernel occupies (to leave CUs to
+    // other work on the device); a cap the shape does not fit in selects the
+    // multi-kernel path.
+    if (const char* e = getenv("SQUIRREL_STEP_GRID")) {
+        const int cap = atoi(e);
+        if (cap > 0 && cap < grid) grid = cap;
+    }
     if (!decode_step_fits(g.dim, g.ffn, g.n_heads, g.n_kv_heads, grid)) return 0;
     const int QD = g.n_heads * g.head_dim, KVD = g.n_kv_heads * g.head_dim;
     std::vector<StepLayer> hl(g.n_layers);

@@ -79,10 +79,10 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a.astype(np.float64) - b) / np.linalg.norm(b))
 
 
-def check_logits(path, seq, got, label):
-    want = run_oracle(path, seq, O.W8A8)
-    f32 = run_oracle(path, seq, O.W8A32)
-    neon = run_oracle(path, seq, O.W8A8_NEON)
+def check_logits(path, seq, got, label, max_pos=256):
+    want = run_oracle(path, seq, O.W8A8, max_pos)
+    f32 = run_oracle(path, seq, O.W8A32, max_pos)
+    neon = run_oracle(path, seq, O.W8A8_NEON, max_pos)
     rows = []
     for step, (g, w, f, n) in enumerate(zip(got, want, f32, neon)):
         rows.append((step, rel_l2(g, w), rel_l2(g, f), rel_l2(w, f), rel_l2(n, w),
@@ -165,6 +165,22 @@ def test_persistent_step_across_attention_tiles(tiny_gguf, wtype):
     assert c.persistent
     rows = check_logits(path, seq, got, f"{wtype}/tiles")
     assert len(rows) == 81
+    for g, t in zip(got, toks):
+        assert t == O.greedy(g)
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+def test_persistent_step_multi_tile_chunks(tiny_gguf, wtype, monkeypatch):
+    """On a 32-CU grid, contexts past 16 tiles give each (KV head, chunk)
+    item several 64-position tiles (an online softmax inside the item), and
+    chunks of unequal length, before the merge phase."""
+    monkeypatch.setenv("SQUIRREL_STEP_GRID", "32")
+    path = tiny_gguf(wtype, "g2")
+    seq = teacher_seq(1000, n_prompt=1050, n_decode=40, seed=13)
+    got, toks, (m, c) = run_gpu(path, seq, max_pos=1100)
+    assert c.persistent
+    rows = check_logits(path, seq, got, f"{wtype}/chunks", max_pos=1100)
+    assert len(rows) == 41
     for g, t in zip(got, toks):
         assert t == O.greedy(g)
 
