@@ -730,11 +730,25 @@ __device__ __forceinline__ ActQ xw_block(const unsigned* xw, int nblk, int blk) 
 // 32..63 are two blocks) and publish them: payload words q[blk*8 + j] and
 // scale words s[blk] (f32 of the fp16 scale), blk = block0 + (lane >> 5).
 // Lanes with `valid` false hold no element (their half is not published).
+// The block maxima and the byte packing move values between lanes with DPP
+// and lane reads only: LDS permutes would queue behind the ring traffic.
 __device__ __forceinline__ void quant_put(float v, int lane, int block0, u64* q, u64* s, unsigned tag, bool valid) {
-    const float amax = fmaxf(sq_half_max(fabsf(valid ? v : 0.0f)), 0.0f);
+    float m = fabsf(valid ? v : 0.0f);
+    m = fmaxf(m, dpp_mov<0xB1, 0xF>(m));   // quad_perm [1,0,3,2]
+    m = fmaxf(m, dpp_mov<0x4E, 0xF>(m));   // quad_perm [2,3,0,1]
+    m = fmaxf(m, dpp_mov<0x141, 0xF>(m));  // row_half_mirror
+    m = fmaxf(m, dpp_mov<0x140, 0xF>(m));  // row_mirror: every lane holds its row's maximum
+    // row_bcast:15 into rows 1 and 3 (rows 0 and 2 keep theirs): lanes 31
+    // and 63 hold the maxima of lanes 0..31 and 32..63
+    m = fmaxf(m, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, m),
+                                                                      __builtin_bit_cast(int, m), 0x142, 0xA, 0xF,
+                                                                      false)));
+    const float lo = lane_value(m, 31), hi = lane_value(m, 63);
+    const float amax = fmaxf(lane < 32 ? lo : hi, 0.0f);
     const float sc = sq_q8_scale(amax);
     const int qv = valid ? ((int)sq_q8_quant(v, sq_q8_inv(sc)) & 0xFF) : 0;
-    const int b1 = __shfl_down(qv, 1, 64), b2 = __shfl_down(qv, 2, 64), b3 = __shfl_down(qv, 3, 64);
+    // bytes of lanes 4k+1, 4k+2, 4k+3 to lane 4k: quad_perm [1,1,1,1], [2,2,2,2], [3,3,3,3]
+    const int b1 = dpp_int<0x55>(qv), b2 = dpp_int<0xAA>(qv), b3 = dpp_int<0xFF>(qv);
     const int blk = block0 + (lane >> 5);
     if ((lane & 3) == 0 && valid)
         put(q + (size_t)blk * 8 + ((lane & 31) >> 2), (unsigned)(qv | (b1 << 8) | (b2 << 16) | (b3 << 24)), tag);
@@ -749,14 +763,31 @@ __device__ __forceinline__ void arg_merge(float& bv, int& bi, int& bn, float v, 
     bn = n > bn ? n : bn;
 }
 
+// (value, index, NaN index) over the wavefront, in every lane.  arg_merge is
+// the maximum under a total order, so the merge order is free: the DPP
+// butterfly of wave_total, where lanes a step does not write keep their own
+// triple (merging a triple with itself leaves it unchanged).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_keep(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void arg_step(float& bv, int& bi, int& bn) {
+    const float ov = __builtin_bit_cast(float, dpp_keep<CTRL, ROWS>(__builtin_bit_cast(int, bv)));
+    const int oi = dpp_keep<CTRL, ROWS>(bi);
+    const int on = dpp_keep<CTRL, ROWS>(bn);
+    arg_merge(bv, bi, bn, ov, oi, on);
+}
 __device__ __forceinline__ void wave_arg(float& bv, int& bi, int& bn) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        const int on = __shfl_xor(bn, o, 64);
-        arg_merge(bv, bi, bn, ov, oi, on);
-    }
+    arg_step<0xB1, 0xF>(bv, bi, bn);   // quad_perm [1,0,3,2]
+    arg_step<0x4E, 0xF>(bv, bi, bn);   // quad_perm [2,3,0,1]
+    arg_step<0x141, 0xF>(bv, bi, bn);  // row_half_mirror
+    arg_step<0x140, 0xF>(bv, bi, bn);  // row_mirror
+    arg_step<0x142, 0xA>(bv, bi, bn);  // row_bcast:15 into rows 1 and 3
+    arg_step<0x143, 0xC>(bv, bi, bn);  // row_bcast:31 into rows 2 and 3: lane 63 holds the result
+    bv = lane_value(bv, 63);
+    bi = __builtin_amdgcn_readlane(bi, 63);
+    bn = __builtin_amdgcn_readlane(bn, 63);
 }
 
 // Phase tags: layer l, phase j in [0, 6): QKV, attention, tile merge, o, gate/up, down.
