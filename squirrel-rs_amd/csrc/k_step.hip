@@ -10,7 +10,10 @@
 // will multiply them (per layer: QKV rows, o rows, gate/up rows, down rows;
 // then its LM-head rows), as one contiguous range of HBM.  A row of k
 // elements is its block payloads (k bytes Q8_0, k/2 bytes Q4_0) followed by
-// its fp16 block scales (k/16 bytes), counted in 16-byte units.
+// its fp16 block scales (k/16 bytes), counted in 16-byte units.  A Q8_0 row
+// holds the first 16 bytes of every block, then the second 16 bytes of every
+// block, so that the lanes of a wavefront (lane = block) read consecutive
+// units.
 //
 // Roles inside a workgroup (6 wavefronts):
 // * Two loader wavefronts copy the CU's stream into a 96 KB LDS ring with
@@ -382,8 +385,10 @@ template <int WT>
 __device__ __forceinline__ RowData row_fetch(const StepShared& S, unsigned rb, int P, int blk) {
     RowData r;
     if constexpr (WT == WT_Q8_0) {
-        r.w0 = *(const uint4*)(S.ring + ring_wrap(rb + 2 * blk) * 16);
-        r.w1 = *(const uint4*)(S.ring + ring_wrap(rb + 2 * blk + 1) * 16);
+        // first halves of the row's blocks, then second halves: lanes read
+        // consecutive units, conflict-free across the LDS banks
+        r.w0 = *(const uint4*)(S.ring + ring_wrap(rb + blk) * 16);
+        r.w1 = *(const uint4*)(S.ring + ring_wrap(rb + (P >> 1) + blk) * 16);
     } else {
         r.w0 = *(const uint4*)(S.ring + ring_wrap(rb + blk) * 16);
         r.w1 = r.w0;
@@ -1505,7 +1510,10 @@ __global__ __launch_bounds__(256) void build_stream_kernel(StepArgs a, uint8_t* 
         }
     }
     const int pu = stream_row_units(WT, m.k) - m.k / 256;  // payload units of a row
-    const uint8_t* src = ur < pu ? (const uint8_t*)m.qs + (size_t)row * pu * 16 + (size_t)ur * 16
+    // Q8_0: stream unit j < pu/2 is the first half of block j, unit pu/2 + j
+    // its second half
+    const int us = WT == WT_Q8_0 && ur < pu ? (ur < pu / 2 ? 2 * ur : 2 * (ur - pu / 2) + 1) : ur;
+    const uint8_t* src = ur < pu ? (const uint8_t*)m.qs + (size_t)row * pu * 16 + (size_t)us * 16
                                  : (const uint8_t*)m.scale + (size_t)row * (m.k / 16) + (size_t)(ur - pu) * 16;
     *(uint4*)(dst + ((size_t)wg * a.stream_stride + u) * 16) = *(const uint4*)src;
 }
