@@ -1250,18 +1250,18 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 stamp(l, TS_GU_IN);
                 const ActQ A = act_lane(S, D);
                 const int pu = stream_row_units(WT, D) - D / 256;
-                // rows i = cw + NCW r < 64, four per batch
+                // rows i = cw + NCW r < 64, eight per batch
                 const int ng_w = (64 - cw + NCW - 1) / NCW;
 #pragma unroll 1
-                for (int r0 = 0; r0 < ng_w; r0 += 4) {
-                    const int n = min(4, ng_w - r0);
-                    float res[4];
-                    if (!dot_batch(std::integral_constant<int, 4>{}, lb + g.offg, g.ua, pu, r0, n, KB, A, res))
+                for (int r0 = 0; r0 < ng_w; r0 += 8) {
+                    const int n = min(8, ng_w - r0);
+                    float res[8];
+                    if (!dot_batch(std::integral_constant<int, 8>{}, lb + g.offg, g.ua, pu, r0, n, KB, A, res))
                         return fail();
                     consumed(lb + g.offg + (cw + NCW * (r0 + n - 1) + 1) * g.ua);
                     if (lane == 0) {
 #pragma unroll
-                        for (int r = 0; r < 4; r++)
+                        for (int r = 0; r < 8; r++)
                             if (r < n) S.gu[cw + NCW * (r0 + r)] = res[r];
                     }
                 }
