@@ -1,4 +1,7 @@
 // Multi-row matmul for the batched prefill: out[m, n] (+)= in[m, :] . W[n, :].
+// The integer path (Q8_0 activations) runs on MFMA (gemm_mfma_kernel below)
+// from one 64-row tile of activations up; the kernel described next serves
+// shorter inputs and f32 activations.
 //
 // A tile of MT activation rows is staged in LDS once; each wavefront then
 // streams weight rows (lane = 32-block, as in the decode matvec) and dots
@@ -170,6 +173,168 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(MatView w, const int8_
     }
 }
 
+// ---- integer path on the matrix cores ------------------------------------------
+// out[m, n] (+)= sum over blocks b of (f32(isum_b[m, n]) * sa[m, b]) * sw[n, b]
+// (dot_q8_0_q8_0_scalar / dot_q8_0_q4_0_scalar, dot_prod.rs:376-403, per
+// output element): isum_b is the exact i32 dot of one 32-element block, which
+// is one v_mfma_i32_16x16x32_i8 (K = 32) for a 16 x 16 tile of outputs.
+//
+// A workgroup computes a 64 x 64 tile of (activation rows) x (weight rows)
+// with four wavefronts of 32 x 32 (2 x 2 MFMA tiles).  K advances in chunks
+// of four blocks: the chunk's activation and weight bytes (64 rows x 128 B
+// each, Q4_0 nibbles expanded to q - 8 as int8) and block scales are staged
+// in LDS, rows MQ_LD bytes apart so that the 16 rows a wavefront's fragment
+// loads touch spread over the banks.  MFMA operand layout (checked on the
+// device): lane l supplies row l % 16, bytes 8 (l / 16) .. +7 of the block;
+// result element r of lane l is row 4 (l / 16) + r, column l % 16.
+constexpr int MQ_T = 64;           // tile rows (activations) and columns (weights)
+constexpr int MQ_KB = 4;           // blocks per K chunk
+constexpr int MQ_KC = MQ_KB * 32;  // bytes per row per K chunk
+constexpr int MQ_LD = MQ_KC + 8;   // LDS row stride in bytes
+
+typedef int mq_v4i __attribute__((ext_vector_type(4)));
+
+template <int WT>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t* __restrict__ aq,
+                                                        const uint16_t* __restrict__ ad, int m_rows,
+                                                        float* __restrict__ out, int ldo, int accumulate) {
+    __shared__ __attribute__((aligned(16))) int8_t sA[MQ_T * MQ_LD];
+    __shared__ __attribute__((aligned(16))) int8_t sW[MQ_T * MQ_LD];
+    __shared__ float sSa[MQ_T][MQ_KB];
+    __shared__ float sSw[MQ_T][MQ_KB];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int K = w.k, KB = K >> 5;
+    const int m0 = blockIdx.y * MQ_T, n0 = blockIdx.x * MQ_T;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int fr = lane & 15, fk = 8 * (lane >> 4);  // fragment row, byte offset in the block
+
+    float acc[2][2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
+
+    // This thread's share of a chunk: activation (and Q8_0 weight) pieces
+    // tid and tid + 256 of 64 rows x 8 sixteen-byte pieces, or one packed
+    // Q4_0 block (row tid / 4, block tid % 4); the scales of row tid / 4,
+    // block tid % 4.  The next chunk's share is loaded into registers while
+    // the current one is multiplied.
+    sq_v4i ra[2], rw[2];
+    uint16_t rsa, rsw;
+    auto fetch = [&](int kb0) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int p = tid + 256 * q, r = p >> 3, s = p & 7;
+            const int k = kb0 * 32 + 16 * s;
+            ra[q] = sq_v4i{0, 0, 0, 0};
+            if (m0 + r < m_rows && k < K) ra[q] = *(const sq_v4i*)(aq + (size_t)(m0 + r) * K + k);
+            if constexpr (WT == WT_Q8_0) {
+                rw[q] = sq_v4i{0, 0, 0, 0};
+                if (n0 + r < w.rows && k < K) rw[q] = *(const sq_v4i*)((const int8_t*)w.qs + (size_t)(n0 + r) * K + k);
+            }
+        }
+        const int r = tid >> 2, kb = kb0 + (tid & 3);
+        if constexpr (WT == WT_Q4_0) {
+            rw[0] = sq_v4i{(int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888};  // q = 8: zero weights
+            if (n0 + r < w.rows && kb < KB) rw[0] = *(const sq_v4i*)((const uint8_t*)w.qs + (size_t)(n0 + r) * (K / 2) + kb * 16);
+        }
+        rsa = (m0 + r < m_rows && kb < KB) ? ad[(size_t)(m0 + r) * KB + kb] : (uint16_t)0;
+        rsw = (n0 + r < w.rows && kb < KB) ? w.scale[(size_t)(n0 + r) * KB + kb] : (uint16_t)0;
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int p = tid + 256 * q, r = p >> 3, s = p & 7;
+            // LDS rows are MQ_LD bytes apart (8-byte aligned): two 8-byte stores
+            int2* da = (int2*)(sA + r * MQ_LD + 16 * s);
+            da[0] = make_int2(ra[q].x, ra[q].y);
+            da[1] = make_int2(ra[q].z, ra[q].w);
+            if constexpr (WT == WT_Q8_0) {
+                int2* dw = (int2*)(sW + r * MQ_LD + 16 * s);
+                dw[0] = make_int2(rw[q].x, rw[q].y);
+                dw[1] = make_int2(rw[q].z, rw[q].w);
+            }
+        }
+        const int r = tid >> 2, b = tid & 3;
+        if constexpr (WT == WT_Q4_0) {
+            // byte j holds element j (low nibble) and element j + 16 (high
+            // nibble); per byte, nibble - 8 as a signed byte: (q | 0x80) - 8
+            // stays within the byte, and xor 0x80 restores the sign
+            const unsigned wd[4] = {(unsigned)rw[0].x, (unsigned)rw[0].y, (unsigned)rw[0].z, (unsigned)rw[0].w};
+            int lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = (int)((((wd[i] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+                hi[i] = (int)(((((wd[i] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+            }
+            int2* dw = (int2*)(sW + r * MQ_LD + 32 * b);
+            dw[0] = make_int2(lo[0], lo[1]);
+            dw[1] = make_int2(lo[2], lo[3]);
+            dw[2] = make_int2(hi[0], hi[1]);
+            dw[3] = make_int2(hi[2], hi[3]);
+        }
+        sSa[r][b] = sq_f16_to_f32(rsa);
+        sSw[r][b] = sq_f16_to_f32(rsw);
+    };
+
+    fetch(0);
+    for (int kb0 = 0; kb0 < KB; kb0 += MQ_KB) {
+        stage();
+        __syncthreads();
+        if (kb0 + MQ_KB < KB) fetch(kb0 + MQ_KB);
+        const int nb = min(MQ_KB, KB - kb0);
+        for (int b = 0; b < nb; b++) {
+            long af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) af[i] = *(const long*)(sA + (wm + 16 * i + fr) * MQ_LD + 32 * b + fk);
+#pragma unroll
+            for (int j = 0; j < 2; j++) bf[j] = *(const long*)(sW + (wn + 16 * j + fr) * MQ_LD + 32 * b + fk);
+            float sa[2][4], sw[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) sa[i][r] = sSa[wm + 16 * i + (fk >> 1) + r][b];
+#pragma unroll
+            for (int j = 0; j < 2; j++) sw[j] = sSw[wn + 16 * j + fr][b];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const mq_v4i zero = {0, 0, 0, 0};
+                    const mq_v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][j][r] += sq_q_term(d[r], sa[i][r], sw[j]);
+                }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm + 16 * i + (fk >> 1) + r, n = n0 + wn + 16 * j + fr;
+                if (m < m_rows && n < w.rows) {
+                    float* o = out + (size_t)m * ldo + n;
+                    *o = accumulate ? *o + acc[i][j][r] : acc[i][j][r];
+                }
+            }
+}
+
+template <int WT>
+int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
+             bool acc) {
+    dim3 grid((w.rows + MQ_T - 1) / MQ_T, (m + MQ_T - 1) / MQ_T);
+    hipLaunchKernelGGL(gemm_mfma_kernel<WT>, grid, dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+    return 0;
+}
+
 template <int WT, bool A8, int NBL, int MT>
 int run(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, const float* x, int m,
         float* out, int ldo, bool acc) {
@@ -204,10 +369,14 @@ int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_
     MatView v = w;
     v.wtype = wtype;
     switch (wtype) {
+        // the integer path runs on the matrix cores
+        // (below one 64-row tile the VALU kernel spreads the weights over more workgroups)
         case WT_Q8_0:
+            if (a8 && m >= MQ_T) return run_mfma<WT_Q8_0>(s, v, aq, ad, m, out, ldo, accumulate);
             return a8 ? dispatch<WT_Q8_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q8_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_Q4_0:
+            if (a8 && m >= MQ_T) return run_mfma<WT_Q4_0>(s, v, aq, ad, m, out, ldo, accumulate);
             return a8 ? dispatch<WT_Q4_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q4_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_BF16:

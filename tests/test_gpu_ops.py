@@ -131,7 +131,7 @@ def term_mag(x, w_f32):
 
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
 @pytest.mark.parametrize("k,n", SHAPES)
-@pytest.mark.parametrize("m", [1, 5])
+@pytest.mark.parametrize("m", [1, 5, 67])
 @pytest.mark.parametrize("f32_acts", [False, True])
 def test_linear_matches_oracle(wtype, k, n, m, f32_acts):
     if wtype == O.BF16 and f32_acts:
