@@ -193,6 +193,7 @@ constexpr int MQ_KC = MQ_KB * 32;  // bytes per row per K chunk
 constexpr int MQ_LD = MQ_KC + 8;   // LDS row stride in bytes
 
 typedef int mq_v4i __attribute__((ext_vector_type(4)));
+typedef float sq_v4f __attribute__((ext_vector_type(4)));
 
 template <int WT>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t* __restrict__ aq,
@@ -200,8 +201,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
                                                         float* __restrict__ out, int ldo, int accumulate) {
     __shared__ __attribute__((aligned(16))) int8_t sA[MQ_T * MQ_LD];
     __shared__ __attribute__((aligned(16))) int8_t sW[MQ_T * MQ_LD];
-    __shared__ float sSa[MQ_T][MQ_KB];
-    __shared__ float sSw[MQ_T][MQ_KB];
+    __shared__ __attribute__((aligned(16))) float sSa[MQ_T][MQ_KB];
+    __shared__ __attribute__((aligned(16))) float sSw[MQ_T][MQ_KB];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = w.k, KB = K >> 5;
@@ -286,19 +287,22 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
         __syncthreads();
         if (kb0 + MQ_KB < KB) fetch(kb0 + MQ_KB);
         const int nb = min(MQ_KB, KB - kb0);
-        for (int b = 0; b < nb; b++) {
+        // the chunk's scales of this lane's rows and columns, all four blocks at once
+        sq_v4f sa4[2][4], sw4[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sa4[i][r] = *(const sq_v4f*)&sSa[wm + 16 * i + (fk >> 1) + r][0];
+#pragma unroll
+        for (int j = 0; j < 2; j++) sw4[j] = *(const sq_v4f*)&sSw[wn + 16 * j + fr][0];
+#pragma unroll
+        for (int b = 0; b < MQ_KB; b++) {
+            if (b >= nb) break;
             long af[2], bf[2];
 #pragma unroll
             for (int i = 0; i < 2; i++) af[i] = *(const long*)(sA + (wm + 16 * i + fr) * MQ_LD + 32 * b + fk);
 #pragma unroll
             for (int j = 0; j < 2; j++) bf[j] = *(const long*)(sW + (wn + 16 * j + fr) * MQ_LD + 32 * b + fk);
-            float sa[2][4], sw[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) sa[i][r] = sSa[wm + 16 * i + (fk >> 1) + r][b];
-#pragma unroll
-            for (int j = 0; j < 2; j++) sw[j] = sSw[wn + 16 * j + fr][b];
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
                     const mq_v4i zero = {0, 0, 0, 0};
                     const mq_v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[i][j][r] += sq_q_term(d[r], sa[i][r], sw[j]);
+                    for (int r = 0; r < 4; r++) acc[i][j][r] += sq_q_term(d[r], sa4[i][r][b], sw4[j][b]);
                 }
         }
         __syncthreads();
