@@ -140,46 +140,67 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     if (tid == 0) atomicExch(&counters[g], 0u);
 }
 
-// Prefill attention: 64 query rows of one head per workgroup, K/V tiles of
-// 64 positions staged in LDS, online softmax.  Thread (ty, tx) owns query
-// rows 4ty..4ty+3 and key columns / output dims 4tx..4tx+3.
+// Prefill attention on the matrix cores, f32 in and out
+// (v_mfma_f32_16x16x4_f32): 64 query rows of one head per workgroup, 16 per
+// wavefront; K and V tiles of 64 positions staged in LDS (V transposed);
+// online softmax per row.
+// MFMA operand layout (checked on the device): lane l supplies A[l % 16][l / 16]
+// and B[l / 16][l % 16]; result r of lane l is D[4 (l / 16) + r][l % 16].
+// The contraction index of step s is 16 (l / 16) + s, so that each lane's 16
+// operands of a 64-long contraction are contiguous in LDS (4 x 16-byte reads).
 constexpr int PT = 64;       // queries and keys per tile
-constexpr int LDP = HD + 4;  // padded LDS row (floats)
+constexpr int ALD = HD + 4;  // padded LDS row (floats)
+typedef float am_v4f __attribute__((ext_vector_type(4)));
+
+// max / sum over the 16 lanes of a DPP row (lanes 16j .. 16j+15), in every lane
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+}
 
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ q,
                                                             const float* __restrict__ kc,
                                                             const float* __restrict__ vc, int pos0,
                                                             int m_rows, int n_heads, int n_kv_heads,
                                                             float* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) float s_q[PT][LDP];
-    __shared__ __attribute__((aligned(16))) float s_k[PT][LDP];
-    __shared__ __attribute__((aligned(16))) float s_v[PT][LDP];
-    __shared__ __attribute__((aligned(16))) float s_p[PT][LDP];
+    __shared__ __attribute__((aligned(16))) float s_k[PT][ALD];      // [key][dim]
+    __shared__ __attribute__((aligned(16))) float s_vt[HD][ALD];     // [dim][key]
+    __shared__ __attribute__((aligned(16))) float s_p[4][16][ALD];   // per wavefront: [row][key]
 
     const int h = blockIdx.x;
     const int t0 = blockIdx.y * PT;
-    const int group = n_heads / n_kv_heads;
-    const int g = h / group;
+    const int g = h / (n_heads / n_kv_heads);
     const int q_dim = n_heads * HD;
     const int kv_dim = n_kv_heads * HD;
-    const int tid = threadIdx.x;
-    const int ty = tid >> 4, tx = tid & 15;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lk = lane >> 4;
     const float scale = 1.0f / sqrtf((float)HD);
 
-    for (int e = tid; e < PT * HD / 4; e += 256) {
-        const int r = e / (HD / 4), c4 = e % (HD / 4);
+    // this lane's query operands: row t0 + 16 wave + li, dims 16 lk .. 16 lk + 15
+    const int qrow = t0 + 16 * wave + li;
+    float qa[16];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (t0 + r < m_rows) v = *(const float4*)(q + (size_t)(t0 + r) * q_dim + h * HD + 4 * c4);
-        *(float4*)&s_q[r][4 * c4] = v;
+        if (qrow < m_rows) v = *(const float4*)(q + (size_t)qrow * q_dim + h * HD + 16 * lk + 4 * c);
+        qa[4 * c] = v.x; qa[4 * c + 1] = v.y; qa[4 * c + 2] = v.z; qa[4 * c + 3] = v.w;
     }
-
-    float mrow[4], lrow[4], o[4][4];
+    // results of this lane: rows t0 + 16 wave + 4 lk + r, dims 16 dt + li
+    float mrow[4], lrow[4];
+    am_v4f o[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        mrow[i] = -INFINITY;
-        lrow[i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) o[i][j] = 0.0f;
+    for (int r = 0; r < 4; r++) {
+        mrow[r] = -INFINITY;
+        lrow[r] = 0.0f;
+        o[r] = am_v4f{0.f, 0.f, 0.f, 0.f};
     }
 
     const int last_q = min(t0 + PT, m_rows) - 1;
@@ -187,91 +208,98 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     for (int k0 = 0; k0 < n_keys; k0 += PT) {
         __syncthreads();
         for (int e = tid; e < PT * HD / 4; e += 256) {
-            const int r = e / (HD / 4), c4 = e % (HD / 4);
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (k0 + r < n_keys) {
-                kv = *(const float4*)(kc + (size_t)(k0 + r) * kv_dim + g * HD + 4 * c4);
-                vv = *(const float4*)(vc + (size_t)(k0 + r) * kv_dim + g * HD + 4 * c4);
+            {   // K: thread e takes row e / 16, dims 4 (e % 16) ..
+                const int r = e >> 4, c4 = e & 15;
+                float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k0 + r < n_keys) kv = *(const float4*)(kc + (size_t)(k0 + r) * kv_dim + g * HD + 4 * c4);
+                *(float4*)&s_k[r][4 * c4] = kv;
             }
-            *(float4*)&s_k[r][4 * c4] = kv;
-            *(float4*)&s_v[r][4 * c4] = vv;
+            {   // V, transposed: thread e takes row e % 64, dims 4 (e / 64) ..
+                const int r = e & 63, c4 = e >> 6;
+                float4 vv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k0 + r < n_keys) vv = *(const float4*)(vc + (size_t)(k0 + r) * kv_dim + g * HD + 4 * c4);
+                s_vt[4 * c4][r] = vv.x;
+                s_vt[4 * c4 + 1][r] = vv.y;
+                s_vt[4 * c4 + 2][r] = vv.z;
+                s_vt[4 * c4 + 3][r] = vv.w;
+            }
         }
         __syncthreads();
 
-        float sc[4][4];
+        // scores of 4 tiles of 16 keys: S[t] = Q K^T over the 64 dims
+        am_v4f sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int t = 0; t < 4; t++) {
+            const float* kr = &s_k[16 * t + li][16 * lk];
+            am_v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; j++) sc[i][j] = 0.0f;
-        for (int d = 0; d < HD; d += 4) {
-            float4 qa[4], kb[4];
+            for (int c = 0; c < 4; c++) {
+                const am_v4f k4 = *(const am_v4f*)(kr + 4 * c);
 #pragma unroll
-            for (int i = 0; i < 4; i++) qa[i] = *(const float4*)&s_q[4 * ty + i][d];
-#pragma unroll
-            for (int j = 0; j < 4; j++) kb[j] = *(const float4*)&s_k[4 * tx + j][d];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    sc[i][j] += qa[i].x * kb[j].x + qa[i].y * kb[j].y + qa[i].z * kb[j].z +
-                                qa[i].w * kb[j].w;
+                for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * c + j], k4[j], acc, 0, 0, 0);
+            }
+            sc[t] = acc;
         }
+        // scale, causal mask (row t sees keys 0 ..= pos0 + t), online softmax
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = t0 + 4 * ty + i;
-            const int limit = pos0 + t;  // inclusive key bound (causal)
+        for (int r = 0; r < 4; r++) {
+            const int tq = t0 + 16 * wave + 4 * lk + r;
+            const int limit = pos0 + tq;
             float rmax = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int kk = k0 + 4 * tx + j;
-                sc[i][j] = (kk <= limit && t < m_rows) ? sc[i][j] * scale : -INFINITY;
-                rmax = fmaxf(rmax, sc[i][j]);
+            for (int t = 0; t < 4; t++) {
+                const int kk = k0 + 16 * t + li;
+                sc[t][r] = (kk <= limit && tq < m_rows) ? sc[t][r] * scale : -INFINITY;
+                rmax = fmaxf(rmax, sc[t][r]);
             }
-#pragma unroll
-            for (int o2 = 8; o2 >= 1; o2 >>= 1) rmax = fmaxf(rmax, __shfl_xor(rmax, o2, 64));
-            const float mn = fmaxf(mrow[i], rmax);
-            const float alpha = (mrow[i] == -INFINITY) ? 0.0f : expf(mrow[i] - mn);
+            rmax = row16_max(rmax);
+            const float mn = fmaxf(mrow[r], rmax);
+            const float alpha = (mrow[r] == -INFINITY) ? 0.0f : expf(mrow[r] - mn);
             float rsum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float p = (sc[i][j] == -INFINITY) ? 0.0f : expf(sc[i][j] - mn);
-                s_p[4 * ty + i][4 * tx + j] = p;
+            for (int t = 0; t < 4; t++) {
+                const float p = (sc[t][r] == -INFINITY) ? 0.0f : expf(sc[t][r] - mn);
+                s_p[wave][4 * lk + r][16 * t + li] = p;
                 rsum += p;
             }
+            rsum = row16_sum(rsum);
+            lrow[r] = lrow[r] * alpha + rsum;
+            mrow[r] = mn;
 #pragma unroll
-            for (int o2 = 8; o2 >= 1; o2 >>= 1) rsum += __shfl_xor(rsum, o2, 64);
-            lrow[i] = lrow[i] * alpha + rsum;
-            mrow[i] = mn;
-#pragma unroll
-            for (int j = 0; j < 4; j++) o[i][j] *= alpha;
+            for (int dt = 0; dt < 4; dt++) o[dt][r] *= alpha;
         }
-        __syncthreads();
-        for (int c = 0; c < PT; c += 4) {
-            float4 pa[4], vb[4];
+        // P back from LDS in the A layout (only this wavefront's lanes wrote it)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+        float pa[16];
 #pragma unroll
-            for (int i = 0; i < 4; i++) pa[i] = *(const float4*)&s_p[4 * ty + i][c];
+        for (int c = 0; c < 4; c++) {
+            const am_v4f p4 = *(const am_v4f*)&s_p[wave][li][16 * lk + 4 * c];
+            pa[4 * c] = p4[0]; pa[4 * c + 1] = p4[1]; pa[4 * c + 2] = p4[2]; pa[4 * c + 3] = p4[3];
+        }
+        // O[dt] += P V over the 64 keys
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++) vb[cc] = *(const float4*)&s_v[c + cc][4 * tx];
+        for (int dt = 0; dt < 4; dt++) {
+            const float* vr = &s_vt[16 * dt + li][16 * lk];
+            am_v4f acc = o[dt];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float pv[4] = {pa[i].x, pa[i].y, pa[i].z, pa[i].w};
+            for (int c = 0; c < 4; c++) {
+                const am_v4f v4 = *(const am_v4f*)(vr + 4 * c);
 #pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    o[i][0] += pv[cc] * vb[cc].x;
-                    o[i][1] += pv[cc] * vb[cc].y;
-                    o[i][2] += pv[cc] * vb[cc].z;
-                    o[i][3] += pv[cc] * vb[cc].w;
-                }
+                for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[4 * c + j], v4[j], acc, 0, 0, 0);
             }
+            o[dt] = acc;
         }
+        // the P reads are done before the next tile's P stores
+        __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = t0 + 4 * ty + i;
-        if (t >= m_rows) continue;
-        const float inv = 1.0f / lrow[i];
-        float4 r = make_float4(o[i][0] * inv, o[i][1] * inv, o[i][2] * inv, o[i][3] * inv);
-        *(float4*)(out + (size_t)t * q_dim + h * HD + 4 * tx) = r;
+    for (int r = 0; r < 4; r++) {
+        const int tq = t0 + 16 * wave + 4 * lk + r;
+        if (tq >= m_rows) continue;
+        const float inv = 1.0f / lrow[r];
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) out[(size_t)tq * q_dim + h * HD + 16 * dt + li] = o[dt][r] * inv;
     }
 }
 
