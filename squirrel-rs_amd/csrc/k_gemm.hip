@@ -174,10 +174,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(MatView w, const int8_
 }
 
 // ---- integer path on the matrix cores ------------------------------------------
-// out[m, n] (+)= sum over blocks b of (f32(isum_b[m, n]) * sa[m, b]) * sw[n, b]
-// (dot_q8_0_q8_0_scalar / dot_q8_0_q4_0_scalar, dot_prod.rs:376-403, per
-// output element): isum_b is the exact i32 dot of one 32-element block, which
-// is one v_mfma_i32_16x16x32_i8 (K = 32) for a 16 x 16 tile of outputs.
+// out[m, n] (+)= sum over blocks b of f32(isum_b[m, n]) * (sa[m, b] * sw[n, b]),
+// each term fused into the running sum as the reference's aarch64 kernels
+// combine blocks (dot_prod.rs:189-252; the scalar twin, dot_prod.rs:376-403,
+// rounds (f32(isum) * sa) * sw instead): isum_b is the exact i32 dot of one
+// 32-element block, which is one v_mfma_i32_16x16x32_i8 (K = 32) for a
+// 16 x 16 tile of outputs.
 //
 // A workgroup computes a 64 x 64 tile of (activation rows) x (weight rows)
 // with four wavefronts of 32 x 32 (2 x 2 MFMA tiles).  K advances in chunks
@@ -310,7 +312,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
                     const mq_v4i zero = {0, 0, 0, 0};
                     const mq_v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[i][j][r] += sq_q_term(d[r], sa4[i][r][b], sw4[j][b]);
+                    for (int r = 0; r < 4; r++) {
+                        // the combine of the reference's aarch64 kernels (dot_prod.rs:189-252):
+                        // acc = fma(f32(isum), sa * sw, acc)
+                        const float sc = sa4[i][r][b] * sw4[j][b];
+                        acc[i][j][r] = fmaf((float)d[r], sc, acc[i][j][r]);
+                    }
                 }
         }
         __syncthreads();
