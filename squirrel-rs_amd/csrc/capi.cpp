@@ -328,7 +328,11 @@ int linear_impl(const float* d_in, size_t m, size_t k, const sq_weight* w, float
         a.out = d_out;
         st = launch_gemv(nullptr, a8 ? PRO_Q8 : PRO_F32, EPI_STORE, a8, a, nullptr);
     } else {
-        st = launch_gemm(nullptr, view(w->m), w->m.wtype, a8, aq, ad, d_in, (int)m, d_out, w->m.rows, false);
+        Tmp ws;  // partial tiles of a K split
+        if ((st = ws.alloc(kGemmSplitFloats * sizeof(float)))) return st;
+        st = launch_gemm(nullptr, view(w->m), w->m.wtype, a8, aq, ad, d_in, (int)m, d_out, w->m.rows, false,
+                         (float*)ws.p, kGemmSplitFloats);
+        if (!st) st = finish(st);  // the workspace is freed on return
     }
     return finish(st);
 }

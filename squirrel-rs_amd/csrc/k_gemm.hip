@@ -200,7 +200,8 @@ typedef float sq_v4f __attribute__((ext_vector_type(4)));
 template <int WT>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t* __restrict__ aq,
                                                         const uint16_t* __restrict__ ad, int m_rows,
-                                                        float* __restrict__ out, int ldo, int accumulate) {
+                                                        float* __restrict__ out, int ldo, int accumulate,
+                                                        int kbs, size_t split_stride) {
     __shared__ __attribute__((aligned(16))) int8_t sA[MQ_T * MQ_LD];
     __shared__ __attribute__((aligned(16))) int8_t sW[MQ_T * MQ_LD];
     __shared__ __attribute__((aligned(16))) float sSa[MQ_T][MQ_KB];
@@ -209,6 +210,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = w.k, KB = K >> 5;
     const int m0 = blockIdx.y * MQ_T, n0 = blockIdx.x * MQ_T;
+    // blocks [kb_begin, kb_end) of K: all of them, or split z of a K split
+    // (its tile goes to a partial buffer, split_stride floats per split)
+    const int kb_begin = blockIdx.z * kbs, kb_end = min(KB, kb_begin + kbs);
+    out += blockIdx.z * split_stride;
     const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     const int fr = lane & 15, fk = 8 * (lane >> 4);  // fragment row, byte offset in the block
 
@@ -233,19 +238,19 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
             const int p = tid + 256 * q, r = p >> 3, s = p & 7;
             const int k = kb0 * 32 + 16 * s;
             ra[q] = sq_v4i{0, 0, 0, 0};
-            if (m0 + r < m_rows && k < K) ra[q] = *(const sq_v4i*)(aq + (size_t)(m0 + r) * K + k);
+            if (m0 + r < m_rows && k < kb_end * 32) ra[q] = *(const sq_v4i*)(aq + (size_t)(m0 + r) * K + k);
             if constexpr (WT == WT_Q8_0) {
                 rw[q] = sq_v4i{0, 0, 0, 0};
-                if (n0 + r < w.rows && k < K) rw[q] = *(const sq_v4i*)((const int8_t*)w.qs + (size_t)(n0 + r) * K + k);
+                if (n0 + r < w.rows && k < kb_end * 32) rw[q] = *(const sq_v4i*)((const int8_t*)w.qs + (size_t)(n0 + r) * K + k);
             }
         }
         const int r = tid >> 2, kb = kb0 + (tid & 3);
         if constexpr (WT == WT_Q4_0) {
             rw[0] = sq_v4i{(int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888};  // q = 8: zero weights
-            if (n0 + r < w.rows && kb < KB) rw[0] = *(const sq_v4i*)((const uint8_t*)w.qs + (size_t)(n0 + r) * (K / 2) + kb * 16);
+            if (n0 + r < w.rows && kb < kb_end) rw[0] = *(const sq_v4i*)((const uint8_t*)w.qs + (size_t)(n0 + r) * (K / 2) + kb * 16);
         }
-        rsa = (m0 + r < m_rows && kb < KB) ? ad[(size_t)(m0 + r) * KB + kb] : (uint16_t)0;
-        rsw = (n0 + r < w.rows && kb < KB) ? w.scale[(size_t)(n0 + r) * KB + kb] : (uint16_t)0;
+        rsa = (m0 + r < m_rows && kb < kb_end) ? ad[(size_t)(m0 + r) * KB + kb] : (uint16_t)0;
+        rsw = (n0 + r < w.rows && kb < kb_end) ? w.scale[(size_t)(n0 + r) * KB + kb] : (uint16_t)0;
     };
     auto stage = [&]() {
 #pragma unroll
@@ -283,12 +288,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
         sSw[r][b] = sq_f16_to_f32(rsw);
     };
 
-    fetch(0);
-    for (int kb0 = 0; kb0 < KB; kb0 += MQ_KB) {
+    fetch(kb_begin);
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += MQ_KB) {
         stage();
         __syncthreads();
-        if (kb0 + MQ_KB < KB) fetch(kb0 + MQ_KB);
-        const int nb = min(MQ_KB, KB - kb0);
+        if (kb0 + MQ_KB < kb_end) fetch(kb0 + MQ_KB);
+        const int nb = min(MQ_KB, kb_end - kb0);
         // the chunk's scales of this lane's rows and columns, all four blocks at once
         sq_v4f sa4[2][4], sw4[2];
 #pragma unroll
@@ -336,12 +341,48 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
             }
 }
 
+// out[r, c] (+)= the sum of the K-split partial tiles, in split order.
+__global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ ws, int splits, size_t stride,
+                                                        int m, int n, float* __restrict__ out, int ldo,
+                                                        int accumulate) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)m * n) return;
+    float v = 0.0f;
+    for (int z = 0; z < splits; z++) v += ws[z * stride + i];
+    float* o = out + (i / n) * (size_t)ldo + i % n;
+    *o = accumulate ? *o + v : v;
+}
+
+// A grid of fewer than 256 tiles (short inputs, narrow matrices) splits K
+// over up to 512 workgroups when the workspace holds the partial tiles; the
+// partials are then summed in a fixed order, so results do not depend on
+// scheduling.
 template <int WT>
 int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
-             bool acc) {
-    dim3 grid((w.rows + MQ_T - 1) / MQ_T, (m + MQ_T - 1) / MQ_T);
-    hipLaunchKernelGGL(gemm_mfma_kernel<WT>, grid, dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0);
-    hipError_t e = hipGetLastError();
+             bool acc, float* ws, size_t ws_floats) {
+    const int gx = (w.rows + MQ_T - 1) / MQ_T, gy = (m + MQ_T - 1) / MQ_T;
+    const int KB = w.k / 32, chunks = (KB + MQ_KB - 1) / MQ_KB;
+    int splits = 1;
+    if (ws != nullptr && gx * gy < 256) {
+        splits = min(chunks, (512 + gx * gy - 1) / (gx * gy));
+        while (splits > 1 && (size_t)splits * m * w.rows > ws_floats) splits--;
+    }
+    const int kbs = ((chunks + splits - 1) / splits) * MQ_KB;  // blocks per split
+    splits = (KB + kbs - 1) / kbs;
+    hipError_t e;
+    if (splits == 1) {
+        hipLaunchKernelGGL(gemm_mfma_kernel<WT>, dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0,
+                           KB, (size_t)0);
+    } else {
+        const size_t stride = (size_t)m * w.rows;
+        hipLaunchKernelGGL(gemm_mfma_kernel<WT>, dim3(gx, gy, splits), dim3(256), 0, s, w, aq, ad, m, ws, w.rows, 0,
+                           kbs, stride);
+        e = hipGetLastError();
+        if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+        hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
+                           m, w.rows, out, ldo, acc ? 1 : 0);
+    }
+    e = hipGetLastError();
     if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
     return 0;
 }
@@ -374,20 +415,21 @@ int dispatch(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
 }  // namespace
 
 int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq, const uint16_t* ad,
-                const float* x, int m, float* out, int ldo, bool accumulate) {
+                const float* x, int m, float* out, int ldo, bool accumulate, float* ws, size_t ws_floats) {
     if (w.k <= 0 || w.k % 32 != 0) return set_error(SQ_ERR_SHAPE, "gemm: k must be a positive multiple of 32");
     if (m <= 0) return set_error(SQ_ERR_EMPTY, "gemm: no rows");
     MatView v = w;
     v.wtype = wtype;
     switch (wtype) {
         // the integer path runs on the matrix cores
-        // (below one 64-row tile the VALU kernel spreads the weights over more workgroups)
+        // (without a workspace for a K split, inputs below one 64-row tile
+        // stay on the VALU kernel, which spreads the weights over more workgroups)
         case WT_Q8_0:
-            if (a8 && m >= MQ_T) return run_mfma<WT_Q8_0>(s, v, aq, ad, m, out, ldo, accumulate);
+            if (a8 && (m >= MQ_T || ws != nullptr)) return run_mfma<WT_Q8_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
             return a8 ? dispatch<WT_Q8_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q8_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_Q4_0:
-            if (a8 && m >= MQ_T) return run_mfma<WT_Q4_0>(s, v, aq, ad, m, out, ldo, accumulate);
+            if (a8 && (m >= MQ_T || ws != nullptr)) return run_mfma<WT_Q4_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
             return a8 ? dispatch<WT_Q4_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q4_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_BF16:

@@ -119,8 +119,12 @@ int launch_copy_i32(hipStream_t s, const int* src, int* dst);
 // ---- prefill matmul (k_gemm.hip) ----------------------------------------
 // out[m, rows] (+)= in[m, k] @ W.  a8: activations given as Q8_0 (aq/ad,
 // [m][k] / [m][k/32]); otherwise f32 activations x [m][k].
+// ws: room for ws_floats floats of partial tiles, for a K split of the
+// integer path when the output has few tiles (null: no split).
+constexpr size_t kGemmSplitFloats = (size_t)4 << 20;
 int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq,
-                const uint16_t* ad, const float* x, int m, float* out, int ldo, bool accumulate);
+                const uint16_t* ad, const float* x, int m, float* out, int ldo, bool accumulate,
+                float* ws = nullptr, size_t ws_floats = 0);
 
 // ---- persistent decode step (k_step.hip) -----------------------------------
 struct StepLayer {

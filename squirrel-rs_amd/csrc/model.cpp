@@ -405,6 +405,7 @@ int ensure_prefill(sq_ctx* c, size_t n) {
         (st = dmalloc(&c->p_act, n * F)) || (st = dmalloc(&c->p_aq, n * wmax)) ||
         (st = dmalloc(&c->p_ad, n * wmax / 32)))
         return st;
+    if (!c->p_split && (st = dmalloc(&c->p_split, kGemmSplitFloats))) return st;
     c->cap_rows = n;
     return 0;
 }
@@ -603,23 +604,25 @@ int run_prefill(sq_ctx* c, size_t n) {
                                       a8 ? c->p_aq : nullptr, c->p_ad)))
             return st;
         if ((st = launch_gemm(s, view(L.qkv), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_qkv,
-                              QD + 2 * KVD, false)))
+                              QD + 2 * KVD, false, c->p_split, kGemmSplitFloats)))
             return st;
         if ((st = launch_rope_kv_rows(s, c->p_qkv, QD + 2 * KVD, N, QD, KVD, hd, pos0, c->rope, c->p_q, kc, vc)))
             return st;
         if ((st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd, c->p_attn))) return st;
         if (a8 && (st = launch_quantize_rows(s, c->p_attn, (size_t)N * QD, c->p_aq, c->p_ad))) return st;
-        if ((st = launch_gemm(s, view(L.o), m->wtype, a8, c->p_aq, c->p_ad, c->p_attn, N, c->p_hidden, D, true)))
+        if ((st = launch_gemm(s, view(L.o), m->wtype, a8, c->p_aq, c->p_ad, c->p_attn, N, c->p_hidden, D, true,
+                              c->p_split, kGemmSplitFloats)))
             return st;
         if ((st = launch_rmsnorm_rows(s, c->p_hidden, L.ffn_norm, N, D, g.eps, a8 ? nullptr : c->p_normed,
                                       a8 ? c->p_aq : nullptr, c->p_ad)))
             return st;
         if ((st = launch_gemm(s, view(L.gateup), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_gu, 2 * F,
-                              false)))
+                              false, c->p_split, kGemmSplitFloats)))
             return st;
         if ((st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, c->p_act, a8 ? c->p_aq : nullptr, c->p_ad)))
             return st;
-        if ((st = launch_gemm(s, view(L.down), m->wtype, a8, c->p_aq, c->p_ad, c->p_act, N, c->p_hidden, D, true)))
+        if ((st = launch_gemm(s, view(L.down), m->wtype, a8, c->p_aq, c->p_ad, c->p_act, N, c->p_hidden, D, true,
+                              c->p_split, kGemmSplitFloats)))
             return st;
     }
     SQ_HIP_CHECK(hipMemcpyAsync(c->hidden, c->p_hidden + (size_t)(N - 1) * D, (size_t)D * 4,
@@ -818,7 +821,7 @@ void ctx_destroy(sq_ctx* c) {
     dfree(c->part_l); dfree(c->part_o); dfree(c->attn_counters); dfree(c->pv); dfree(c->pi); dfree(c->pn); dfree(c->dbg_normed);
     dfree(c->dbg_qs); dfree(c->dbg_d); dfree(c->last_hidden); dfree(c->head_qs); dfree(c->head_d);
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
-    dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad);
+    dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad); dfree(c->p_split);
     dfree(c->d_layers); dfree(c->s_stream); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
     if (c->h_pinned) (void)hipHostFree(c->h_pinned);
     if (c->stream) (void)hipStreamDestroy(c->stream);
