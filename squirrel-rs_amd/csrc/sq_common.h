@@ -87,23 +87,52 @@ __device__ __forceinline__ float sq_bf16_to_f32(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 
+// Wavefront reductions through DPP row operations and lane reads, with no
+// LDS traffic; every lane of the wavefront must be active, and every lane
+// gets the result.  Quad swaps, the half-row and row mirrors leave each lane
+// with its 16-lane row's value; row_bcast:15 / :31 then carry rows into the
+// upper rows, and lanes 31 / 63 are read back.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float sq_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
+}
+// the same, with lanes outside ROWS keeping their own value
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float sq_dpp_keep(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float sq_row_max(float v) {
+    v = fmaxf(v, sq_dpp<0xB1, 0xF>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, sq_dpp<0x4E, 0xF>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, sq_dpp<0x141, 0xF>(v));  // row_half_mirror
+    return fmaxf(v, sq_dpp<0x140, 0xF>(v));  // row_mirror
+}
+
 __device__ __forceinline__ float sq_wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += sq_dpp<0xB1, 0xF>(v);
+    v += sq_dpp<0x4E, 0xF>(v);
+    v += sq_dpp<0x141, 0xF>(v);
+    v += sq_dpp<0x140, 0xF>(v);
+    v += sq_dpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += sq_dpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3: lane 63 holds the sum
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ float sq_wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = sq_row_max(v);
+    v = fmaxf(v, sq_dpp_keep<0x142, 0xA>(v));
+    v = fmaxf(v, sq_dpp_keep<0x143, 0xC>(v));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// Reductions within aligned groups of 32 lanes (one 32-element block).
+// Maximum within each aligned group of 32 lanes (one 32-element block).
 __device__ __forceinline__ float sq_half_max(float v) {
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = sq_row_max(v);
+    v = fmaxf(v, sq_dpp_keep<0x142, 0xA>(v));  // lanes 31 and 63 hold the two halves' maxima
+    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    return (threadIdx.x & 32) ? hi : lo;
 }
 
 // The Q8_0 activation quantizer of the reference, for one element whose block
