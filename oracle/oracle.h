@@ -1,8 +1,8 @@
 /*
  * Oracle: a CPU restatement of squirrel-rs's Llama token loop arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
- * implementation and the timed CPU baseline.  Only tests/, the smoke() entry
+ * TEST INFRASTRUCTURE ONLY.  This library is the reference arithmetic the HIP
+ * implementation is tested against, and the timed CPU baseline.  Only tests/, the smoke() entry
  * and bench.py's cpu_baseline leg may load it; the product path never does.
  *
  * Every function follows one reference function (cited file:line, paths

@@ -15,7 +15,7 @@ from .ops import BLOCK_Q8_0
 
 WTYPES = {"Q8_0": 8, "Q4_0": 2, "BF16": 30}
 
-# Llama-3.2-1B architecture.
+# Llama-3.2-1B architecture (the benchmark workloads).
 LLAMA_1B = dict(n_layers=16, dim=2048, ffn_dim=8192, n_heads=32, n_kv_heads=8, vocab=128256,
                 context_length=131072)
 
