@@ -51,11 +51,28 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(MatView table, const uint
 __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, const float* w, int dim,
                                                                float eps, float* out, int8_t* act_q,
                                                                uint16_t* act_d) {
+    // rows up to 8 * kBlock wide are read once, every load issued before any
+    // arithmetic; wider rows are read twice
+    constexpr int NC = 8;
     __shared__ float s_red[kBlock / 64];
     const int r = blockIdx.x;
     const float* xr = x + (size_t)r * dim;
+    const bool cached = dim <= NC * kBlock;
+    float xv[NC], wv[NC];
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += kBlock) ss += xr[i] * xr[i];
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int i = threadIdx.x + j * kBlock;
+            xv[j] = i < dim ? xr[i] : 0.0f;
+            wv[j] = i < dim ? w[i] : 0.0f;
+        }
+        // the same order as the loop below (elements past dim add 0)
+#pragma unroll
+        for (int j = 0; j < NC; j++) ss += xv[j] * xv[j];
+    } else {
+        for (int i = threadIdx.x; i < dim; i += kBlock) ss += xr[i] * xr[i];
+    }
     ss = sq_wave_sum(ss);
     if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
     __syncthreads();
@@ -64,10 +81,9 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
     const float rms = sqrtf(tot / (float)dim + eps);
     // dim is a multiple of 32 and the stride is a multiple of 64, so every
     // aligned 32-lane group holds one whole block.
-    for (int base = 0; base < dim; base += kBlock) {
-        const int i = base + threadIdx.x;
+    auto emit = [&](int i, float xi, float wi) {
         const bool vi = i < dim;
-        const float y = vi ? (xr[i] * w[i]) / rms : 0.0f;
+        const float y = vi ? (xi * wi) / rms : 0.0f;
         if (vi && out) out[(size_t)r * dim + i] = y;
         if (act_q) {
             float amax = fmaxf(sq_half_max(fabsf(y)), 0.0f);
@@ -77,6 +93,18 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
                 act_q[(size_t)r * dim + i] = sq_q8_quant(y, inv);
                 if ((i & 31) == 0) act_d[((size_t)r * dim + i) >> 5] = sq_f32_to_f16(scale);
             }
+        }
+    };
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            if (j * kBlock >= dim) break;
+            emit(threadIdx.x + j * kBlock, xv[j], wv[j]);
+        }
+    } else {
+        for (int base = 0; base < dim; base += kBlock) {
+            const int i = base + threadIdx.x;
+            emit(i, i < dim ? xr[i] : 0.0f, i < dim ? w[i] : 0.0f);
         }
     }
 }
