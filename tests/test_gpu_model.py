@@ -185,6 +185,21 @@ def test_persistent_step_multi_tile_chunks(tiny_gguf, wtype, monkeypatch):
         assert t == O.greedy(g)
 
 
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+def test_long_prefill_unsplit_matrix_core_tiles(tiny_gguf, wtype):
+    """A 2048-token prompt gives every prefill matmul of the g4 model at least
+    256 output tiles (8 x 32 for the o and down projections), so they run on
+    the matrix cores without the K split, accumulating the residual in place;
+    shorter prompts take the split path."""
+    path = tiny_gguf(wtype, "g4")
+    seq = teacher_seq(2048, n_prompt=2048, n_decode=2, seed=17)
+    got, toks, _ = run_gpu(path, seq, max_pos=2056)
+    rows = check_logits(path, seq, got, f"{wtype}/long prefill", max_pos=2056)
+    assert len(rows) == 3
+    for g, t in zip(got, toks):
+        assert t == O.greedy(g)
+
+
 def test_persistent_deterministic_across_resets(tiny_gguf):
     """Back-to-back generations, with and without a reset in between, give
     the same tokens and logits (barrier epochs carry over between launches)."""
