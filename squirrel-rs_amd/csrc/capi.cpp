@@ -21,10 +21,6 @@ int synth_write(const std::string& path, const sq_synth_spec& s);
 
 using namespace sq;
 
-struct sq_weight {
-    DevMatrix m;
-};
-
 namespace {
 
 // Temporary device buffer for the operator-level entry points.

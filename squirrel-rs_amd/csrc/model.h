@@ -130,6 +130,11 @@ struct sq_ctx {
     std::vector<uint64_t> kernel_bytes;
 };
 
+// A weight matrix uploaded through the operator-level entry points.
+struct sq_weight {
+    sq::DevMatrix m;
+};
+
 namespace sq {
 int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out);
 void ctx_destroy(sq_ctx* c);

@@ -69,6 +69,7 @@ PROTOS = {
     "sq_weight_free": ([vp], None),
     "sq_quantize_row_q8_0": ([vp, sz, vp], i32),
     "sq_linear": ([vp, sz, sz, vp, vp, u32], i32),
+    "sq_linear_noalloc": ([vp, sz, sz, vp, vp, u32], i32),
     "sq_linear_shared": ([vp, sz, sz, vp, vp, sz, u32], i32),
     "sq_block_isums": ([vp, vp, sz, vp], i32),
     "sq_embed": ([vp, sz, vp, vp], i32),
