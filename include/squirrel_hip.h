@@ -143,6 +143,18 @@ int sq_ctx_decode_kernel(const sq_ctx* c);
 int sq_ctx_step_trace(sq_ctx* c, int enable);
 int sq_ctx_step_trace_read(sq_ctx* c, uint64_t* out, size_t n, int* grid, int* stride);
 size_t sq_ctx_seq_len(const sq_ctx* c);
+/* Quantized-activation taps (measurement and parity aid, no reference
+ * counterpart).  The integer path quantizes activations to Q8_0 at four sites
+ * per layer -- the attention-norm output and the attention output (inputs of
+ * linear_shared / linear in layers::attention, src/models/llama/layers.rs:24-58),
+ * the FFN-norm output and the FFN activation (layers::ffn, layers.rs:64-77) --
+ * and once for the LM head.  With taps enabled every forward records them;
+ * the one-kernel-per-op decode step always does.  _read copies those of the
+ * most recent forward (n rows) as GGUF Q8_0 blocks (34 B each): per layer, per
+ * site, n rows of k/32 blocks (k = dim, q_dim, dim, ffn_dim), then the
+ * LM-head input row (dim/32 blocks).  n_blocks must hold them all. */
+int sq_ctx_act_taps(sq_ctx* c, int enable);
+int sq_ctx_act_tap_read(sq_ctx* c, void* blocks, size_t n_blocks);
 
 /* Model::forward (model.rs:45-97): n > 1 runs the batched prefill, n == 1 a
  * decode step.  Asynchronous on the context stream. */

@@ -390,40 +390,63 @@ static size_t row_bytes(int wtype, size_t k) {
     return k * 2;
 }
 
+/* One job covers m rows x n_out columns; task index i is output (i / n_out,
+ * i % n_out).  The reference walks rows serially and columns in parallel
+ * (src/kernels/matmul.rs:28-64); every output element is one independent dot
+ * product either way, so spreading rows over the pool too changes no bit. */
 typedef struct {
-    const float* a_row;            /* f32 activation row (W8A32 / BF16) */
-    const or_block_q8_0* aq_row;   /* quantized activation row (W8A8) */
+    const float* in;               /* f32 activations [m][k] (W8A32 / BF16) */
+    const or_block_q8_0* aq;       /* quantized activations [m][k/32] (W8A8) */
     const uint8_t* w;
-    size_t k, rb;
+    size_t k, rb, n_out;
     int wtype, mode;
-    float* out_row;
+    float* out;
 } linear_job;
 
 static void linear_task(void* p, size_t begin, size_t end) {
     const linear_job* j = (const linear_job*)p;
     size_t nb = j->k / 32;
-    for (size_t c = begin; c < end; c++) {
+    for (size_t i = begin; i < end; i++) {
+        const size_t r = i / j->n_out, c = i % j->n_out;
+        const float* a_row = j->in ? j->in + r * j->k : NULL;
+        const or_block_q8_0* aq_row = j->aq ? j->aq + r * nb : NULL;
         const uint8_t* wr = j->w + c * j->rb;
         float v;
         if (j->wtype == OR_BF16) {
-            v = or_dot_f32_bf16(j->a_row, (const uint16_t*)wr, j->k);
+            v = or_dot_f32_bf16(a_row, (const uint16_t*)wr, j->k);
         } else if (j->mode == OR_W8A32) {
-            v = (j->wtype == OR_Q8_0) ? or_dot_f32_q8_0(j->a_row, (const or_block_q8_0*)wr, nb)
-                                      : or_dot_f32_q4_0(j->a_row, (const or_block_q4_0*)wr, nb);
+            v = (j->wtype == OR_Q8_0) ? or_dot_f32_q8_0(a_row, (const or_block_q8_0*)wr, nb)
+                                      : or_dot_f32_q4_0(a_row, (const or_block_q4_0*)wr, nb);
         } else if (j->mode == OR_W8A8) {
-            v = (j->wtype == OR_Q8_0) ? or_dot_q8_0_q8_0(j->aq_row, (const or_block_q8_0*)wr, nb)
-                                      : or_dot_q8_0_q4_0(j->aq_row, (const or_block_q4_0*)wr, nb);
+            v = (j->wtype == OR_Q8_0) ? or_dot_q8_0_q8_0(aq_row, (const or_block_q8_0*)wr, nb)
+                                      : or_dot_q8_0_q4_0(aq_row, (const or_block_q4_0*)wr, nb);
         } else {
-            v = (j->wtype == OR_Q8_0) ? or_dot_q8_0_q8_0_neon(j->aq_row, (const or_block_q8_0*)wr, nb)
-                                      : or_dot_q8_0_q4_0_neon(j->aq_row, (const or_block_q4_0*)wr, nb);
+            v = (j->wtype == OR_Q8_0) ? or_dot_q8_0_q8_0_neon(aq_row, (const or_block_q8_0*)wr, nb)
+                                      : or_dot_q8_0_q4_0_neon(aq_row, (const or_block_q4_0*)wr, nb);
         }
-        j->out_row[c] = v;
+        j->out[r * j->n_out + c] = v;
     }
 }
 
 /* linear -> linear_blocks -> matmul_f32_q / matmul_prequant_q
  * (src/ops/linear.rs:26-70, src/kernels/matmul.rs:7-24,68-171).
  * Quantized activations are formed for all rows first (matmul.rs:91-98). */
+static int linear_rows(const float* in, const or_block_q8_0* aq, size_t m, size_t k, int wtype,
+                       const void* w, size_t n_out, float* out, int mode) {
+    linear_job j;
+    j.in = in;
+    j.aq = aq;
+    j.n_out = n_out;
+    j.out = out;
+    j.w = (const uint8_t*)w;
+    j.k = k;
+    j.rb = row_bytes(wtype, k);
+    j.wtype = wtype;
+    j.mode = mode;
+    parallel_for(m * n_out, 64, linear_task, &j);
+    return OR_OK;
+}
+
 int or_linear(const float* in, size_t m, size_t k, int wtype, const void* w, size_t n_out,
               float* out, int mode) {
     if (wtype != OR_Q8_0 && wtype != OR_Q4_0 && wtype != OR_BF16) return OR_INVALID_TYPE;
@@ -434,20 +457,19 @@ int or_linear(const float* in, size_t m, size_t k, int wtype, const void* w, siz
         aq = (or_block_q8_0*)malloc(sizeof(or_block_q8_0) * (m * k / 32 + 1));
         or_quantize_row_q8_0(in, m * k, aq);
     }
-    linear_job j;
-    j.w = (const uint8_t*)w;
-    j.k = k;
-    j.rb = row_bytes(wtype, k);
-    j.wtype = wtype;
-    j.mode = mode;
-    for (size_t r = 0; r < m; r++) {
-        j.a_row = in + r * k;
-        j.aq_row = aq ? aq + r * (k / 32) : NULL;
-        j.out_row = out + r * n_out;
-        parallel_for(n_out, 64, linear_task, &j);
-    }
+    int st = linear_rows(in, aq, m, k, wtype, w, n_out, out, mode);
     free(aq);
-    return OR_OK;
+    return st;
+}
+
+/* matmul_prequant_q (src/kernels/matmul.rs:133-171): activations already
+ * quantized (linear_shared quantizes once per projection group,
+ * src/ops/linear.rs:117-127). */
+int or_linear_prequant(const or_block_q8_0* aq, size_t m, size_t k, int wtype, const void* w,
+                       size_t n_out, float* out, int mode) {
+    if (wtype != OR_Q8_0 && wtype != OR_Q4_0) return OR_INVALID_TYPE;
+    if (k % 32 != 0 || mode == OR_W8A32) return OR_SHAPE;
+    return linear_rows(NULL, aq, m, k, wtype, w, n_out, out, mode);
 }
 
 int or_block_isums(const or_block_q8_0* a, int wtype, const void* w_row, size_t nblocks,
@@ -671,6 +693,7 @@ struct or_ctx {
     /* workspace (src/models/common/workspace.rs:10-50) */
     float *hidden, *normed, *q, *kk, *vv, *attn, *attn_out, *gate, *up, *ffn_act, *ffn_out;
     float *last_hidden, *logits;
+    or_block_q8_0* aq; /* quantized activations of one site (rows x widest k / 32) */
 };
 
 or_ctx* or_ctx_new(const or_llama* m, size_t max_positions, int mode) {
@@ -702,6 +725,10 @@ static void ctx_prepare(or_ctx* c, const or_llama* m, size_t seq) {
         free(*bufs[i]);
         *bufs[i] = (float*)calloc(seq * widths[i], sizeof(float));
     }
+    size_t kmax = (size_t)m->ffn_dim > q_dim ? (size_t)m->ffn_dim : q_dim;
+    if ((size_t)m->dim > kmax) kmax = (size_t)m->dim;
+    free(c->aq);
+    c->aq = (or_block_q8_0*)calloc(seq * kmax / 32 + 1, sizeof(or_block_q8_0));
     c->cap_rows = seq;
 }
 
@@ -716,6 +743,7 @@ void or_ctx_free(or_ctx* c) {
     float* bufs[] = {c->hidden, c->normed, c->q, c->kk, c->vv, c->attn, c->attn_out,
                      c->gate, c->up, c->ffn_act, c->ffn_out, c->last_hidden, c->logits};
     for (int i = 0; i < 13; i++) free(bufs[i]);
+    free(c->aq);
     free(c);
 }
 
@@ -724,13 +752,88 @@ size_t or_ctx_seq_len(const or_ctx* c) { return c->seq_len; }
 const float* or_ctx_logits(const or_ctx* c) { return c->logits; }
 const float* or_ctx_last_hidden(const or_ctx* c) { return c->last_hidden; }
 
+/* Phase lock (see oracle.h): compare the device's blocks of one site with
+ * the oracle's own, count, and continue with the device's. */
+static void lock_site(or_lock* lk, const float* x, size_t rows, size_t k, or_block_q8_0* own,
+                      const or_block_q8_0* dev, int layer, int site) {
+    size_t nb = rows * k / 32;
+    for (size_t b = 0; b < nb; b++) {
+        const float* xb = x + b * 32;
+        lk->values += 32;
+        if (own[b].d == dev[b].d && memcmp(own[b].qs, dev[b].qs, 32) == 0) continue;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(xb[i]));
+        float scale = amax / 127.0f;
+        float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+        int ok = 1;
+        size_t bad_i = 0;
+        float bad_dist = 0.0f;
+        if (own[b].d != dev[b].d) {
+            /* adjacent binary16 values of one sign, and the oracle's f32 scale
+             * at their rounding midpoint */
+            int adjacent = ((own[b].d ^ dev[b].d) & 0x8000) == 0 &&
+                           (own[b].d > dev[b].d ? own[b].d - dev[b].d : dev[b].d - own[b].d) == 1;
+            float mid = 0.5f * (or_f16_to_f32(own[b].d) + or_f16_to_f32(dev[b].d));
+            if (!adjacent || fabsf(scale - mid) > 1e-5f * fabsf(mid)) {
+                ok = 0;
+                bad_i = b * 32;
+                bad_dist = -1.0f;
+            } else {
+                lk->scale_flips++;
+            }
+        }
+        for (int i = 0; i < 32 && ok; i++) {
+            int qo = own[b].qs[i], qd = dev[b].qs[i];
+            if (qo == qd) continue;
+            float v = fabsf(xb[i] * inv);
+            float dist = fabsf((v - floorf(v)) - 0.5f);
+            if ((qo - qd == 1 || qd - qo == 1) && dist <= lk->tol) {
+                lk->flips++;
+            } else {
+                ok = 0;
+                bad_i = b * 32 + (size_t)i;
+                bad_dist = dist;
+            }
+        }
+        if (!ok) {
+            if (lk->bad == 0) {
+                lk->first_bad_layer = layer;
+                lk->first_bad_site = site;
+                lk->first_bad_index = bad_i;
+                lk->first_bad_dist = bad_dist;
+            }
+            lk->bad++;
+        }
+        own[b] = dev[b];
+    }
+}
+
+/* The quantized activations of one site: the oracle's own, or under a lock
+ * the device's after the check; dev advances past the site's blocks. */
+static const or_block_q8_0* site_blocks(or_ctx* c, const float* x, size_t rows, size_t k, or_lock* lk,
+                                        const or_block_q8_0** dev, int layer, int site) {
+    or_quantize_row_q8_0(x, rows * k, c->aq);
+    if (lk) {
+        lock_site(lk, x, rows, k, c->aq, *dev, layer, site);
+        *dev += rows * k / 32;
+    }
+    return c->aq;
+}
+
 int or_forward(const or_llama* m, or_ctx* c, const uint32_t* ids, size_t n) {
+    return or_forward_locked(m, c, ids, n, NULL);
+}
+
+int or_forward_locked(const or_llama* m, or_ctx* c, const uint32_t* ids, size_t n, or_lock* lock) {
     if (n == 0) return OR_EMPTY;
     if (c->seq_len + n > c->max_pos) return 5;
     size_t D = (size_t)m->dim, F = (size_t)m->ffn_dim, hd = (size_t)m->head_dim;
     size_t q_dim = (size_t)m->n_heads * hd, kv_dim = (size_t)m->n_kv_heads * hd;
     int mode = c->mode, wt = m->wtype;
+    int int_acts = wt != OR_BF16 && mode != OR_W8A32;
     int st;
+    if (lock && !int_acts) return OR_INVALID_TYPE;
+    const or_block_q8_0* dev = lock ? lock->blocks : NULL;
     ctx_prepare(c, m, n);
     st = or_embed(ids, n, wt, m->tok_embd, D, (size_t)m->vocab, c->hidden);
     if (st) return st;
@@ -739,11 +842,18 @@ int or_forward(const or_llama* m, or_ctx* c, const uint32_t* ids, size_t n) {
         const void* const* L = m->layer + 9 * l;
         /* attention half (layers.rs:89-96) */
         or_rms_norm_rows(c->hidden, (const float*)L[0], c->normed, n, D, m->eps);
-        /* linear_shared over q,k,v: quantizing once or per weight gives the
-         * same blocks, so three linear calls are equivalent. */
-        if ((st = or_linear(c->normed, n, D, wt, L[1], q_dim, c->q, mode))) return st;
-        if ((st = or_linear(c->normed, n, D, wt, L[2], kv_dim, c->kk, mode))) return st;
-        if ((st = or_linear(c->normed, n, D, wt, L[3], kv_dim, c->vv, mode))) return st;
+        /* linear_shared over q,k,v: the input is quantized once
+         * (linear.rs:117-127) */
+        if (int_acts) {
+            const or_block_q8_0* a = site_blocks(c, c->normed, n, D, lock, &dev, l, 0);
+            if ((st = or_linear_prequant(a, n, D, wt, L[1], q_dim, c->q, mode))) return st;
+            if ((st = or_linear_prequant(a, n, D, wt, L[2], kv_dim, c->kk, mode))) return st;
+            if ((st = or_linear_prequant(a, n, D, wt, L[3], kv_dim, c->vv, mode))) return st;
+        } else {
+            if ((st = or_linear(c->normed, n, D, wt, L[1], q_dim, c->q, mode))) return st;
+            if ((st = or_linear(c->normed, n, D, wt, L[2], kv_dim, c->kk, mode))) return st;
+            if ((st = or_linear(c->normed, n, D, wt, L[3], kv_dim, c->vv, mode))) return st;
+        }
         or_rope_rows(c->q, n, q_dim, position, m->inv_freq, hd / 2);
         or_rope_rows(c->kk, n, kv_dim, position, m->inv_freq, hd / 2);
         memcpy(c->k[l] + position * kv_dim, c->kk, sizeof(float) * n * kv_dim);
@@ -751,20 +861,40 @@ int or_forward(const or_llama* m, or_ctx* c, const uint32_t* ids, size_t n) {
         st = or_sdpa(c->q, c->k[l], c->v[l], c->attn, n, position + n, (size_t)m->n_heads,
                      (size_t)m->n_kv_heads, hd);
         if (st) return st;
-        if ((st = or_linear(c->attn, n, q_dim, wt, L[4], D, c->attn_out, mode))) return st;
+        if (int_acts) {
+            const or_block_q8_0* a = site_blocks(c, c->attn, n, q_dim, lock, &dev, l, 1);
+            if ((st = or_linear_prequant(a, n, q_dim, wt, L[4], D, c->attn_out, mode))) return st;
+        } else if ((st = or_linear(c->attn, n, q_dim, wt, L[4], D, c->attn_out, mode))) {
+            return st;
+        }
         for (size_t i = 0; i < n * D; i++) c->hidden[i] += c->attn_out[i];
         /* FFN half (layers.rs:98-106, 64-77) */
         or_rms_norm_rows(c->hidden, (const float*)L[5], c->normed, n, D, m->eps);
-        if ((st = or_linear(c->normed, n, D, wt, L[6], F, c->gate, mode))) return st;
-        if ((st = or_linear(c->normed, n, D, wt, L[7], F, c->up, mode))) return st;
+        if (int_acts) {
+            const or_block_q8_0* a = site_blocks(c, c->normed, n, D, lock, &dev, l, 2);
+            if ((st = or_linear_prequant(a, n, D, wt, L[6], F, c->gate, mode))) return st;
+            if ((st = or_linear_prequant(a, n, D, wt, L[7], F, c->up, mode))) return st;
+        } else {
+            if ((st = or_linear(c->normed, n, D, wt, L[6], F, c->gate, mode))) return st;
+            if ((st = or_linear(c->normed, n, D, wt, L[7], F, c->up, mode))) return st;
+        }
         or_silu(c->gate, n * F);
         for (size_t i = 0; i < n * F; i++) c->ffn_act[i] = c->gate[i] * c->up[i];
-        if ((st = or_linear(c->ffn_act, n, F, wt, L[8], D, c->ffn_out, mode))) return st;
+        if (int_acts) {
+            const or_block_q8_0* a = site_blocks(c, c->ffn_act, n, F, lock, &dev, l, 3);
+            if ((st = or_linear_prequant(a, n, F, wt, L[8], D, c->ffn_out, mode))) return st;
+        } else if ((st = or_linear(c->ffn_act, n, F, wt, L[8], D, c->ffn_out, mode))) {
+            return st;
+        }
         for (size_t i = 0; i < n * D; i++) c->hidden[i] += c->ffn_out[i];
     }
     c->seq_len += n;
     /* Final norm over every row, then only the last row feeds the head
      * (model.rs:72-95). */
     or_rms_norm_rows(c->hidden + (n - 1) * D, m->output_norm, c->last_hidden, 1, D, m->eps);
+    if (int_acts) {
+        const or_block_q8_0* a = site_blocks(c, c->last_hidden, 1, D, lock, &dev, m->n_layers, 0);
+        return or_linear_prequant(a, 1, D, wt, m->output, (size_t)m->vocab, c->logits, mode);
+    }
     return or_linear(c->last_hidden, 1, D, wt, m->output, (size_t)m->vocab, c->logits, mode);
 }

@@ -128,6 +128,33 @@ const float* or_ctx_logits(const or_ctx* c);
 /* Debug views of the most recent forward: the final normed last row. */
 const float* or_ctx_last_hidden(const or_ctx* c);
 
+/* matmul_prequant_q (src/kernels/matmul.rs:133-171): linear on activations
+ * already quantized to Q8_0 blocks (m rows of k/32 blocks). */
+int or_linear_prequant(const or_block_q8_0* aq, size_t m, size_t k, int wtype, const void* w,
+                       size_t n_out, float* out, int mode);
+
+/* Phase lock of the integer path.  Every quantization site of a forward
+ * (per layer: 0 the attention-norm output, 1 the attention output, 2 the
+ * FFN-norm output, 3 the FFN activation, each n rows; then site 0 of layer
+ * n_layers, the final norm's last row) is quantized by the oracle and
+ * compared block by block with an implementation's blocks, given in that
+ * order in `blocks`.  An element may differ by one step only where the
+ * oracle's scaled value x * (1/scale) lies within `tol` quanta of a rounding
+ * midpoint (a flip that any f32 rounding difference upstream can cause); a
+ * block scale may differ by one binary16 step only where the f32 scale lies
+ * at the midpoint of the two.  Everything else counts as bad.  The forward
+ * then continues with the implementation's blocks, so the logits compare the
+ * two at f32 rounding level.  Integer modes only. */
+typedef struct {
+    const or_block_q8_0* blocks;
+    float tol;
+    uint64_t values, flips, scale_flips, bad;
+    int first_bad_layer, first_bad_site;
+    size_t first_bad_index;
+    float first_bad_dist; /* distance from the midpoint, -1 for a scale mismatch */
+} or_lock;
+int or_forward_locked(const or_llama* m, or_ctx* c, const uint32_t* ids, size_t n, or_lock* lock);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,7 @@ def lib():
         L.or_ctx_seq_len.argtypes = [vp]
         L.or_ctx_seq_len.restype = sz
         L.or_forward.argtypes = [vp, vp, vp, sz]
+        L.or_forward_locked.argtypes = [vp, vp, vp, sz, C.POINTER(OrLock)]
         L.or_ctx_logits.argtypes = [vp]
         L.or_ctx_logits.restype = f32p
         L.or_ctx_last_hidden.argtypes = [vp]
@@ -315,6 +316,14 @@ class _Llama(C.Structure):
                 ("inv_freq", C.c_void_p)]
 
 
+class OrLock(C.Structure):
+    """or_lock (oracle.h): the phase lock of a forward's quantization sites."""
+    _fields_ = [("blocks", C.c_void_p), ("tol", C.c_float), ("values", C.c_uint64),
+                ("flips", C.c_uint64), ("scale_flips", C.c_uint64), ("bad", C.c_uint64),
+                ("first_bad_layer", C.c_int), ("first_bad_site", C.c_int),
+                ("first_bad_index", C.c_size_t), ("first_bad_dist", C.c_float)]
+
+
 class OracleModel:
     """Llama3_2 over a GGUF file (model.rs:20-110, weights.rs:50-97)."""
 
@@ -359,11 +368,30 @@ class OracleContext:
         self.m = model
         self.h = lib().or_ctx_new(C.byref(model.s), max_positions, mode)
 
-    def forward(self, ids) -> None:
+    def forward(self, ids, lock=None, tol: float = 0.02):
+        """One Llama3_2::forward.  With `lock` (an implementation's Q8_0
+        blocks of every quantization site, oracle.h or_lock order) the
+        integer path checks each site against its own quantization and then
+        continues with the given blocks; returns the lock's counts."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
-        st = lib().or_forward(C.byref(self.m.s), self.h, _p(ids), ids.size)
+        if lock is None:
+            st = lib().or_forward(C.byref(self.m.s), self.h, _p(ids), ids.size)
+            if st:
+                raise RuntimeError(f"oracle forward status {st}")
+            return None
+        blocks = np.ascontiguousarray(lock)
+        c = self.m.cfg
+        width = 2 * c.embed_dim + c.n_heads * c.head_dim + c.ffn_dim
+        need = (ids.size * c.n_blocks * width + c.embed_dim) // 32
+        if blocks.dtype != BLOCK_Q8_0 or blocks.size != need:
+            raise ValueError(f"lock needs {need} Q8_0 blocks, got {blocks.size}")
+        lk = OrLock(blocks.ctypes.data, tol)
+        st = lib().or_forward_locked(C.byref(self.m.s), self.h, _p(ids), ids.size, C.byref(lk))
         if st:
             raise RuntimeError(f"oracle forward status {st}")
+        return {"values": lk.values, "flips": lk.flips, "scale_flips": lk.scale_flips, "bad": lk.bad,
+                "first_bad": (lk.first_bad_layer, lk.first_bad_site, lk.first_bad_index, lk.first_bad_dist)
+                if lk.bad else None}
 
     def logits(self) -> np.ndarray:
         p = lib().or_ctx_logits(self.h)

@@ -195,6 +195,16 @@ int sq_ctx_step_trace_read(sq_ctx* c, uint64_t* out, size_t n, int* grid, int* s
 
 size_t sq_ctx_seq_len(const sq_ctx* c) { return c ? c->seq_len : 0; }
 
+int sq_ctx_act_taps(sq_ctx* c, int enable) {
+    if (!c) return set_error(SQ_ERR_ARG, "act_taps: null context");
+    return ctx_set_taps(c, enable != 0);
+}
+
+int sq_ctx_act_tap_read(sq_ctx* c, void* blocks, size_t n_blocks) {
+    if (!c || !blocks) return set_error(SQ_ERR_ARG, "act_tap_read: null argument");
+    return ctx_read_taps(c, blocks, n_blocks);
+}
+
 int sq_forward(const sq_model* m, sq_ctx* c, const uint32_t* ids, size_t n) {
     if (!m || !c || c->m != m) return set_error(SQ_ERR_ARG, "forward: context does not belong to this model");
     return ctx_forward(c, ids, n);
@@ -233,8 +243,8 @@ int sq_ctx_debug_act(sq_ctx* c, float* normed, void* blocks) {
     if (blocks) {
         std::vector<int8_t> qs(D);
         std::vector<uint16_t> d(D / 32);
-        SQ_HIP_CHECK(hipMemcpy(qs.data(), c->dbg_qs, D, hipMemcpyDeviceToHost));
-        SQ_HIP_CHECK(hipMemcpy(d.data(), c->dbg_d, D / 32 * 2, hipMemcpyDeviceToHost));
+        SQ_HIP_CHECK(hipMemcpy(qs.data(), c->tap_q, D, hipMemcpyDeviceToHost));
+        SQ_HIP_CHECK(hipMemcpy(d.data(), c->tap_d, D / 32 * 2, hipMemcpyDeviceToHost));
         uint8_t* o = (uint8_t*)blocks;
         for (size_t b = 0; b < D / 32; b++) {
             memcpy(o + b * 34, &d[b], 2);

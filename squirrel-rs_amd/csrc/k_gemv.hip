@@ -207,7 +207,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         for (int w = 0; w < WAVES; w++) tot += s_red[w];
         const float mean = tot / (float)K;
         const float rms = sqrtf(mean + a.eps);
-        const bool dbg = (a.dbg_normed != nullptr) && blockIdx.x == 0;
+        const bool tap_y = a.dbg_normed != nullptr && blockIdx.x == 0;
+        const bool tap_q = a.dbg_qs != nullptr && blockIdx.x == 0;
 #pragma unroll
         for (int j = 0; j < G::EPT; j++) {
             const int i = tid + j * G::NT;
@@ -228,14 +229,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
                     for (int o = 16; o >= 1; o >>= 1) qi += __shfl_xor(qi, o, 64);
                     if (vi && (i & 31) == 0) s_asum[i >> 5] = qi;
                 }
-                if (dbg && vi) {
-                    a.dbg_normed[i] = y;
+                if (tap_y && vi) a.dbg_normed[i] = y;
+                if (tap_q && vi) {
                     a.dbg_qs[i] = q;
                     if ((i & 31) == 0) a.dbg_d[i >> 5] = sq_f32_to_f16(scale);
                 }
             } else {
                 if (vi) s_x[(i >> 5) * kPad + (i & 31)] = y;
-                if (dbg && vi) a.dbg_normed[i] = y;
+                if (tap_y && vi) a.dbg_normed[i] = y;
             }
         }
         __syncthreads();

@@ -605,7 +605,9 @@ __device__ __forceinline__ int dpp_int(int v) {
 // sum of squares is reduced per wavefront, then across the wavefronts in a
 // fixed order after a compute-group barrier; the four threads of a 32-block
 // (a lane quad) agree on its scale through DPP and the blocks land in
-// S.aq / S.as / S.asum.  Ends with a compute-group barrier; false: abandon.
+// S.aq / S.as / S.asum (and, when non-null, the f32 row in dbg_y and the
+// blocks in dbg_q / dbg_d).  Ends with a compute-group barrier; false:
+// abandon.
 template <typename Embed>
 __device__ __forceinline__ bool norm_quant(StepShared& S, const u64* src, unsigned tag, Embed&& embed, const Gains& G,
                                            int D, float eps, float* dbg_y, int8_t* dbg_q, uint16_t* dbg_d, int& gen,
@@ -674,10 +676,10 @@ __device__ __forceinline__ bool norm_quant(StepShared& S, const u64* src, unsign
         }
         if (dbg_y) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                dbg_y[8 * t + e] = y[e];
-                dbg_q[8 * t + e] = (int8_t)((packed[e >> 2] >> (8 * (e & 3))) & 0xFF);
-            }
+            for (int e = 0; e < 8; e++) dbg_y[8 * t + e] = y[e];
+        }
+        if (dbg_q) {
+            *(int2*)(dbg_q + 8 * t) = make_int2(packed[0], packed[1]);
             if ((t & 3) == 0) dbg_d[blk] = d16;
         }
     }
@@ -855,6 +857,10 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     const int nchunks = (ntiles + tpc - 1) / tpc;
     const Xchg X = a.x;
     const cptr<StepLayer> LY = (cptr<StepLayer>)a.layers;
+    // quantized-activation taps (sq_ctx::tap_q layout): per layer, sites of
+    // width D, QD, D, F
+    const size_t TW = 2 * (size_t)D + QD + F;
+    const bool tapping = a.taps != 0 && wg == 0;
     int gen = 0;  // compute-group barrier count
     auto next_xw = [&]() -> unsigned* { return S.xw; };
 
@@ -965,10 +971,11 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                     }
                 }
                 const Gains gn = load_gains(LY[l].attn_norm, D);
-                const bool dbg = l == 0 && wg == 0 && a.dbg_normed != nullptr;
+                const bool tap0 = wg == 0 && (l == 0 || tapping);
                 stamp(l, TS_QKV_POLL);
                 if (!norm_quant(S, l == 0 ? nullptr : X.h, l == 0 ? 0u : tag(l - 1, PH_DOWN), embed_at, gn, D, a.eps,
-                                dbg ? a.dbg_normed : nullptr, a.dbg_qs, a.dbg_d, gen, C))
+                                (l == 0 && wg == 0) ? a.dbg_normed : nullptr, tap0 ? a.dbg_qs + l * TW : nullptr,
+                                tap0 ? a.dbg_d + l * TW / 32 : nullptr, gen, C))
                     return;
                 stamp(l, TS_QKV_IN);
                 const ActQ A = act_lane(S, D);
@@ -1219,6 +1226,12 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 unsigned* xw = next_xw();
                 if (!gather(S, xw, X.a, QD / 4 + QB, Tin, C, gen)) return;
                 stamp(l, TS_O_IN);
+                if (tapping) {  // the attention output's blocks
+                    const gptr<int> tq = (gptr<int>)gl(a.dbg_qs + l * TW + D);
+                    const gptr<uint16_t> td = gl(a.dbg_d + (l * TW + D) / 32);
+                    for (int i = tid; i < QD / 4; i += CNT) tq[i] = (int)xw[i];
+                    for (int i = tid; i < QB; i += CNT) td[i] = sq_f32_to_f16(__builtin_bit_cast(float, xw[QD / 4 + i]));
+                }
                 if (n_own > 0) {
                     const ActQ A = xw_block<WT>(xw, QB, lane);
                     float res[RMAX];
@@ -1245,7 +1258,9 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
             if (g.ng > 0) {
                 const Gains gn = load_gains(LY[l].ffn_norm, D);
                 const long long rw0 = ring_wait;
-                if (!norm_quant(S, X.h, tag(l, PH_O), embed_at, gn, D, a.eps, nullptr, nullptr, nullptr, gen, C))
+                if (!norm_quant(S, X.h, tag(l, PH_O), embed_at, gn, D, a.eps, nullptr,
+                                tapping ? a.dbg_qs + l * TW + D + QD : nullptr,
+                                tapping ? a.dbg_d + (l * TW + D + QD) / 32 : nullptr, gen, C))
                     return;
                 stamp(l, TS_GU_IN);
                 const ActQ A = act_lane(S, D);
@@ -1294,6 +1309,12 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 unsigned* xw = next_xw();
                 if (!gather(S, xw, X.f, F / 4 + FB, tag(l, PH_GU), C, gen)) return;
                 stamp(l, TS_DOWN_IN);
+                if (tapping) {  // the FFN activation's blocks
+                    const gptr<int> tq = (gptr<int>)gl(a.dbg_qs + l * TW + 2 * D + QD);
+                    const gptr<uint16_t> td = gl(a.dbg_d + (l * TW + 2 * D + QD) / 32);
+                    for (int i = tid; i < F / 4; i += CNT) tq[i] = (int)xw[i];
+                    for (int i = tid; i < FB; i += CNT) td[i] = sq_f32_to_f16(__builtin_bit_cast(float, xw[F / 4 + i]));
+                }
                 if (n_own > 0) {
                     const int pu = stream_row_units(WT, F) - F / 256;
                     if (!ensure(lb + g.offd + (cw + NCW * (n_own - 1) + 1) * g.ud)) return fail();
@@ -1355,7 +1376,7 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
         const Gains gn = load_gains(a.out_norm, D);
         const bool dbg = wg == 0 && a.last_hidden != nullptr;
         if (!norm_quant(S, X.h, tag(a.n_layers - 1, PH_DOWN), embed_at, gn, D, a.eps, dbg ? a.last_hidden : nullptr,
-                        a.head_qs, a.head_d, gen, C))
+                        dbg ? a.head_qs : nullptr, dbg ? a.head_d : nullptr, gen, C))
             return;
         stamp(a.n_layers, 0);
         const ActQ A = act_lane(S, D);

@@ -51,7 +51,8 @@ struct GemvArgs {
     MatView embd;
     const uint32_t* token;
     float* hidden_out;
-    // debug taps of the prologue (workgroup 0 only, when non-null)
+    // taps of the prologue, written by workgroup 0 when non-null: the
+    // normalized row (f32) and, on the integer path, its Q8_0 blocks
     float* dbg_normed;
     int8_t* dbg_qs;
     uint16_t* dbg_d;
@@ -177,8 +178,12 @@ struct StepArgs {
     int* error;
     long long spin_limit;
     float* dbg_normed;  // layer-0 attention norm (workgroup 0), optional
+    // Quantized activations of every site (the context's tap_q / tap_d
+    // layout): layer 0's attention-norm site always, every site when taps
+    // is non-zero (written by workgroup 0).
     int8_t* dbg_qs;
     uint16_t* dbg_d;
+    int taps;
     float* last_hidden;  // final norm (workgroup 0), optional
     int8_t* head_qs;
     uint16_t* head_d;

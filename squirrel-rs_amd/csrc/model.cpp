@@ -432,6 +432,10 @@ int build_decode_step(sq_ctx* c) {
     std::vector<int> named(K_COUNT, -1);
 
     const size_t kv_layer = c->max_pos * (size_t)KVD;
+    const size_t TW = tap_width(g);
+    // quantized activations of layer l, site j (see sq_ctx::tap_q)
+    auto tq = [&](int l, int j) { return c->tap_q + l * TW + tap_offset(g, j); };
+    auto td = [&](int l, int j) { return c->tap_d + (l * TW + tap_offset(g, j)) / 32; };
     auto mat_bytes = [](const DevMatrix& x) { return (uint64_t)(x.payload_bytes() + x.scale_bytes()); };
     // Kernels replayed by the measurement entry point come from layer 1 (layer
     // 0's QKV also performs the embedding lookup).
@@ -454,14 +458,14 @@ int build_decode_step(sq_ctx* c) {
         q.q_rows = QD;
         q.kv_rows = KVD;
         q.half = g.head_dim / 2;
+        q.dbg_qs = a8 ? tq(l, 0) : nullptr;
+        q.dbg_d = td(l, 0);
         if (l == 0) {
             // embed (model.rs:57-62) fused into the first norm prologue
             q.embd = view(m->embd);
             q.token = c->d_token;
             q.hidden_out = c->hidden;
             q.dbg_normed = c->dbg_normed;
-            q.dbg_qs = c->dbg_qs;
-            q.dbg_d = c->dbg_d;
         }
         if (l == lt) {
             named[K_QKV] = (int)step.size();
@@ -472,16 +476,17 @@ int build_decode_step(sq_ctx* c) {
             named[K_ATTN] = (int)step.size();
             c->kernel_bytes[K_ATTN] = 0;  // depends on the position; filled at measurement time
         }
+        int8_t* const attn_q = a8 ? tq(l, 1) : nullptr;
+        uint16_t* const attn_d = td(l, 1);
         step.push_back([=]() {
             return launch_attn_decode(s, c->q, kc, vc, c->d_pos, g.n_heads, g.n_kv_heads, g.head_dim, c->max_tiles,
-                                      c->part_m, c->part_l, c->part_o, c->attn_counters, c->attn,
-                                      a8 ? c->attn_q : nullptr, c->attn_d);
+                                      c->part_m, c->part_l, c->part_o, c->attn_counters, c->attn, attn_q, attn_d);
         });
         GemvArgs o{};
         o.w = view(Ly.o);
         o.n_rows = D;
-        o.aq = c->attn_q;
-        o.ad = c->attn_d;
+        o.aq = tq(l, 1);
+        o.ad = td(l, 1);
         o.x = c->attn;
         o.out = c->hidden;
         if (l == lt) {
@@ -496,8 +501,10 @@ int build_decode_step(sq_ctx* c) {
         gu.norm_w = Ly.ffn_norm;
         gu.eps = g.eps;
         gu.ffn_act = c->ffn_act;
-        gu.act_q = a8 ? c->ffn_q : nullptr;
-        gu.act_d = c->ffn_d;
+        gu.act_q = a8 ? tq(l, 3) : nullptr;
+        gu.act_d = td(l, 3);
+        gu.dbg_qs = a8 ? tq(l, 2) : nullptr;
+        gu.dbg_d = td(l, 2);
         if (l == lt) {
             named[K_GATEUP] = (int)step.size();
             c->kernel_bytes[K_GATEUP] = mat_bytes(Ly.gateup) + 2ull * D * 4 + (uint64_t)F * 4 +
@@ -507,8 +514,8 @@ int build_decode_step(sq_ctx* c) {
         GemvArgs dn{};
         dn.w = view(Ly.down);
         dn.n_rows = D;
-        dn.aq = c->ffn_q;
-        dn.ad = c->ffn_d;
+        dn.aq = tq(l, 3);
+        dn.ad = td(l, 3);
         dn.x = c->ffn_act;
         dn.out = c->hidden;
         if (l == lt) {
@@ -591,6 +598,24 @@ int run_prefill(sq_ctx* c, size_t n) {
     hipStream_t s = c->stream;
     int st;
     if ((st = ensure_prefill(c, n))) return st;
+    const size_t TW = tap_width(g);
+    const bool taps = c->taps && a8;
+    if (taps && c->ptap_rows < n) {
+        dfree(c->ptap_q);
+        dfree(c->ptap_d);
+        c->ptap_rows = 0;
+        if ((st = dmalloc(&c->ptap_q, n * g.n_layers * TW)) || (st = dmalloc(&c->ptap_d, n * g.n_layers * TW / 32)))
+            return st;
+        c->ptap_rows = n;
+    }
+    // the n rows of site j of layer l, just quantized into p_aq / p_ad
+    auto tap = [&](int l, int j, size_t k) -> int {
+        if (!taps) return 0;
+        const size_t off = n * (l * TW + tap_offset(g, j));
+        SQ_HIP_CHECK(hipMemcpyAsync(c->ptap_q + off, c->p_aq, n * k, hipMemcpyDeviceToDevice, s));
+        SQ_HIP_CHECK(hipMemcpyAsync(c->ptap_d + off / 32, c->p_ad, n * k / 16, hipMemcpyDeviceToDevice, s));
+        return 0;
+    };
     SQ_HIP_CHECK(hipMemcpyAsync(c->d_ids, c->h_pinned, n * 4, hipMemcpyHostToDevice, s));
     if ((st = launch_embed(s, view(m->embd), m->wtype, c->d_ids, (int)n, D, c->p_hidden))) return st;
     const int pos0 = (int)c->seq_len;
@@ -601,7 +626,8 @@ int run_prefill(sq_ctx* c, size_t n) {
         float* kc = c->kcache + l * kv_layer;
         float* vc = c->vcache + l * kv_layer;
         if ((st = launch_rmsnorm_rows(s, c->p_hidden, L.attn_norm, N, D, g.eps, a8 ? nullptr : c->p_normed,
-                                      a8 ? c->p_aq : nullptr, c->p_ad)))
+                                      a8 ? c->p_aq : nullptr, c->p_ad)) ||
+            (st = tap(l, 0, D)))
             return st;
         if ((st = launch_gemm(s, view(L.qkv), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_qkv,
                               QD + 2 * KVD, false, c->p_split, kGemmSplitFloats)))
@@ -609,17 +635,20 @@ int run_prefill(sq_ctx* c, size_t n) {
         if ((st = launch_rope_kv_rows(s, c->p_qkv, QD + 2 * KVD, N, QD, KVD, hd, pos0, c->rope, c->p_q, kc, vc)))
             return st;
         if ((st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd, c->p_attn))) return st;
-        if (a8 && (st = launch_quantize_rows(s, c->p_attn, (size_t)N * QD, c->p_aq, c->p_ad))) return st;
+        if (a8 && ((st = launch_quantize_rows(s, c->p_attn, (size_t)N * QD, c->p_aq, c->p_ad)) || (st = tap(l, 1, QD))))
+            return st;
         if ((st = launch_gemm(s, view(L.o), m->wtype, a8, c->p_aq, c->p_ad, c->p_attn, N, c->p_hidden, D, true,
                               c->p_split, kGemmSplitFloats)))
             return st;
         if ((st = launch_rmsnorm_rows(s, c->p_hidden, L.ffn_norm, N, D, g.eps, a8 ? nullptr : c->p_normed,
-                                      a8 ? c->p_aq : nullptr, c->p_ad)))
+                                      a8 ? c->p_aq : nullptr, c->p_ad)) ||
+            (st = tap(l, 2, D)))
             return st;
         if ((st = launch_gemm(s, view(L.gateup), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_gu, 2 * F,
                               false, c->p_split, kGemmSplitFloats)))
             return st;
-        if ((st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, c->p_act, a8 ? c->p_aq : nullptr, c->p_ad)))
+        if ((st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, c->p_act, a8 ? c->p_aq : nullptr, c->p_ad)) ||
+            (a8 && (st = tap(l, 3, F))))
             return st;
         if ((st = launch_gemm(s, view(L.down), m->wtype, a8, c->p_aq, c->p_ad, c->p_act, N, c->p_hidden, D, true,
                               c->p_split, kGemmSplitFloats)))
@@ -703,8 +732,9 @@ int setup_persistent(sq_ctx* c) {
     a.error = c->s_error;
     a.spin_limit = (long long)khz * 250;  // 250 ms
     a.dbg_normed = c->dbg_normed;
-    a.dbg_qs = c->dbg_qs;
-    a.dbg_d = c->dbg_d;
+    a.dbg_qs = c->tap_q;
+    a.dbg_d = c->tap_d;
+    a.taps = c->taps ? 1 : 0;
     a.last_hidden = c->last_hidden;
     a.head_qs = c->head_qs;
     a.head_d = c->head_d;
@@ -755,17 +785,17 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
         (st = dmalloc(&c->vcache, (size_t)g.n_layers * max_pos * KVD)) || (st = dmalloc(&c->rope, max_pos * half)) ||
         (st = dmalloc(&c->d_pos, 1)) || (st = dmalloc(&c->d_token, 1)) || (st = dmalloc(&c->d_ids, max_pos)) ||
         (st = dmalloc(&c->d_hist, max_pos + 1)) || (st = dmalloc(&c->d_nhist, 1)) || (st = dmalloc(&c->hidden, D)) ||
-        (st = dmalloc(&c->q, QD)) || (st = dmalloc(&c->attn, QD)) || (st = dmalloc(&c->attn_q, QD)) ||
-        (st = dmalloc(&c->attn_d, QD / 32)) || (st = dmalloc(&c->ffn_act, F)) || (st = dmalloc(&c->ffn_q, F)) ||
-        (st = dmalloc(&c->ffn_d, F / 32)) || (st = dmalloc(&c->logits, (size_t)g.vocab)) ||
+        (st = dmalloc(&c->q, QD)) || (st = dmalloc(&c->attn, QD)) || (st = dmalloc(&c->ffn_act, F)) ||
+        (st = dmalloc(&c->tap_q, g.n_layers * tap_width(g))) ||
+        (st = dmalloc(&c->tap_d, g.n_layers * tap_width(g) / 32)) || (st = dmalloc(&c->logits, (size_t)g.vocab)) ||
         (st = dmalloc(&c->part_m, (size_t)g.n_heads * c->max_tiles)) ||
         (st = dmalloc(&c->part_l, (size_t)g.n_heads * c->max_tiles)) ||
         (st = dmalloc(&c->part_o, (size_t)g.n_heads * c->max_tiles * g.head_dim)) ||
         (st = dmalloc(&c->attn_counters, (size_t)g.n_kv_heads)) ||
         (st = dmalloc(&c->pv, c->n_parts)) ||
         (st = dmalloc(&c->pi, c->n_parts)) || (st = dmalloc(&c->pn, c->n_parts)) ||
-        (st = dmalloc(&c->dbg_normed, D)) || (st = dmalloc(&c->dbg_qs, D)) || (st = dmalloc(&c->dbg_d, D / 32)) ||
-        (st = dmalloc(&c->last_hidden, D)) || (st = dmalloc(&c->head_qs, D)) || (st = dmalloc(&c->head_d, D / 32)))
+        (st = dmalloc(&c->dbg_normed, D)) || (st = dmalloc(&c->last_hidden, D)) || (st = dmalloc(&c->head_qs, D)) ||
+        (st = dmalloc(&c->head_d, D / 32)))
         return fail(st);
     he = hipHostMalloc((void**)&c->h_pinned, (max_pos + 16) * sizeof(uint32_t), hipHostMallocDefault);
     if (he != hipSuccess) return fail(set_error(SQ_ERR_HIP, std::string("hipHostMalloc: ") + hipGetErrorString(he)));
@@ -816,10 +846,10 @@ void ctx_destroy(sq_ctx* c) {
     if (c->graph) (void)hipGraphExecDestroy(c->graph);
     if (c->graph_def) (void)hipGraphDestroy(c->graph_def);
     dfree(c->kcache); dfree(c->vcache); dfree(c->rope); dfree(c->d_pos); dfree(c->d_token); dfree(c->d_ids);
-    dfree(c->d_hist); dfree(c->d_nhist); dfree(c->hidden); dfree(c->q); dfree(c->attn); dfree(c->attn_q);
-    dfree(c->attn_d); dfree(c->ffn_act); dfree(c->ffn_q); dfree(c->ffn_d); dfree(c->logits); dfree(c->part_m);
+    dfree(c->d_hist); dfree(c->d_nhist); dfree(c->hidden); dfree(c->q); dfree(c->attn); dfree(c->tap_q);
+    dfree(c->tap_d); dfree(c->ffn_act); dfree(c->ptap_q); dfree(c->ptap_d); dfree(c->logits); dfree(c->part_m);
     dfree(c->part_l); dfree(c->part_o); dfree(c->attn_counters); dfree(c->pv); dfree(c->pi); dfree(c->pn); dfree(c->dbg_normed);
-    dfree(c->dbg_qs); dfree(c->dbg_d); dfree(c->last_hidden); dfree(c->head_qs); dfree(c->head_d);
+    dfree(c->last_hidden); dfree(c->head_qs); dfree(c->head_d);
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
     dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad); dfree(c->p_split);
     dfree(c->d_layers); dfree(c->s_stream); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
@@ -848,6 +878,40 @@ int ctx_forward(sq_ctx* c, const uint32_t* ids, size_t n) {
     }
     if (st) return st;
     c->seq_len += n;
+    c->last_rows = n;
+    c->last_tapped = c->a8 && (n > 1 ? c->taps : (c->taps || !c->persist));
+    return 0;
+}
+
+int ctx_set_taps(sq_ctx* c, bool on) {
+    if (!c->a8) return set_error(SQ_ERR_UNSUPPORTED, "act_taps: the context has no quantized activations");
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    c->taps = on;
+    c->step.taps = on ? 1 : 0;
+    return 0;
+}
+
+int ctx_read_taps(sq_ctx* c, void* blocks, size_t n_blocks) {
+    const Config& g = c->m->cfg;
+    const size_t TW = tap_width(g), n = c->last_rows, D = g.dim;
+    if (n == 0 || !c->last_tapped)
+        return set_error(SQ_ERR_ARG, "act_tap_read: the most recent forward did not record its activations");
+    const size_t body = n * g.n_layers * TW;  // elements before the LM-head row
+    if (n_blocks < (body + D) / 32) return set_error(SQ_ERR_ARG, "act_tap_read: buffer too small");
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    std::vector<int8_t> qs(body + D);
+    std::vector<uint16_t> d((body + D) / 32);
+    const int8_t* sq = n > 1 ? c->ptap_q : c->tap_q;
+    const uint16_t* sd = n > 1 ? c->ptap_d : c->tap_d;
+    SQ_HIP_CHECK(hipMemcpy(qs.data(), sq, body, hipMemcpyDeviceToHost));
+    SQ_HIP_CHECK(hipMemcpy(d.data(), sd, body / 16, hipMemcpyDeviceToHost));
+    SQ_HIP_CHECK(hipMemcpy(qs.data() + body, c->head_qs, D, hipMemcpyDeviceToHost));
+    SQ_HIP_CHECK(hipMemcpy(d.data() + body / 32, c->head_d, D / 16, hipMemcpyDeviceToHost));
+    uint8_t* out = (uint8_t*)blocks;
+    for (size_t b = 0; b < (body + D) / 32; b++) {
+        memcpy(out + 34 * b, &d[b], 2);
+        memcpy(out + 34 * b + 2, qs.data() + 32 * b, 32);
+    }
     return 0;
 }
 

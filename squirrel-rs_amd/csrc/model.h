@@ -77,12 +77,23 @@ struct sq_ctx {
     float* hidden = nullptr;
     float* q = nullptr;
     float* attn = nullptr;
-    int8_t* attn_q = nullptr;
-    uint16_t* attn_d = nullptr;
     float* ffn_act = nullptr;
-    int8_t* ffn_q = nullptr;
-    uint16_t* ffn_d = nullptr;
     float* logits = nullptr;
+    // Q8_0 activations of every quantization site of a decode step, per
+    // layer l at l * tap_width: the attention-norm output [dim], the attention
+    // output [q_dim], the FFN-norm output [dim], the FFN activation [ffn]
+    // (payload tap_q, fp16 block scales tap_d at the same offset / 32).  The
+    // one-kernel-per-op step reads its activations from here; the persistent
+    // step writes layer 0's attention-norm site, and every site when taps
+    // are on.  The LM-head input is head_qs / head_d.
+    int8_t* tap_q = nullptr;
+    uint16_t* tap_d = nullptr;
+    bool taps = false;             // record every site (persistent step, prefill)
+    int8_t* ptap_q = nullptr;      // the prefill's sites: rows x the decode layout
+    uint16_t* ptap_d = nullptr;
+    size_t ptap_rows = 0;
+    size_t last_rows = 0;          // rows of the most recent forward
+    bool last_tapped = false;      // its sites were recorded
     float *part_m = nullptr, *part_l = nullptr, *part_o = nullptr;
     int max_tiles = 0;               // 64-position attention tiles of max_pos
     unsigned* attn_counters = nullptr;  // one per kv head, zero between launches
@@ -91,8 +102,6 @@ struct sq_ctx {
     int* pn = nullptr;
     int n_parts = 0;
     float* dbg_normed = nullptr;   // layer-0 attention norm of the last decode step
-    int8_t* dbg_qs = nullptr;
-    uint16_t* dbg_d = nullptr;
     float* last_hidden = nullptr;  // final norm of the last forward
     int8_t* head_qs = nullptr;
     uint16_t* head_d = nullptr;
@@ -130,6 +139,17 @@ struct sq_ctx {
     std::vector<uint64_t> kernel_bytes;
 };
 
+namespace sq {
+// Quantization sites of one layer, in activation elements: the
+// attention-norm output, the attention output, the FFN-norm output and the
+// FFN activation; tap_width is their sum.
+inline size_t tap_width(const Config& g) { return 2 * (size_t)g.dim + (size_t)g.n_heads * g.head_dim + g.ffn; }
+inline size_t tap_offset(const Config& g, int site) {
+    const size_t D = g.dim, QD = (size_t)g.n_heads * g.head_dim;
+    return site == 0 ? 0 : site == 1 ? D : site == 2 ? D + QD : 2 * D + QD;
+}
+}  // namespace sq
+
 // A weight matrix uploaded through the operator-level entry points.
 struct sq_weight {
     sq::DevMatrix m;
@@ -142,6 +162,10 @@ int ctx_forward(sq_ctx* c, const uint32_t* ids, size_t n);
 int ctx_generate(sq_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t max_tokens, uint32_t flags,
                  uint32_t* out, size_t* n_out, double* step_ms);
 int ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes);
+int ctx_set_taps(sq_ctx* c, bool on);
+// Host copy of the most recent forward's quantized activations as GGUF
+// Q8_0 blocks: per layer, per site, rows x k/32 blocks; then the LM-head row.
+int ctx_read_taps(sq_ctx* c, void* blocks, size_t n_blocks);
 // Status of the persistent decode step's error word (synchronizes the stream).
 int ctx_check(sq_ctx* c);
 int model_load(const char* path, sq_model** out);

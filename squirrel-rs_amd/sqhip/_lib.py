@@ -56,6 +56,8 @@ PROTOS = {
     "sq_ctx_free": ([vp], None),
     "sq_ctx_reset": ([vp], i32),
     "sq_ctx_seq_len": ([vp], sz),
+    "sq_ctx_act_taps": ([vp, i32], i32),
+    "sq_ctx_act_tap_read": ([vp, vp, sz], i32),
     "sq_ctx_decode_kernel": ([vp], i32),
     "sq_ctx_step_trace": ([vp, i32], i32),
     "sq_ctx_step_trace_read": ([vp, vp, sz, C.POINTER(i32), C.POINTER(i32)], i32),

@@ -112,6 +112,22 @@ class ModelContext:
     def forward(self, token_ids) -> None:
         ids = np.ascontiguousarray(token_ids, dtype=np.uint32)
         check(lib().sq_forward(self.model.h, self.h, ids.ctypes.data, ids.size))
+        self._last_rows = ids.size
+
+    def act_taps(self, enable: bool = True) -> None:
+        """Record the quantized activations of every site of each forward."""
+        check(lib().sq_ctx_act_taps(self.h, 1 if enable else 0))
+
+    def act_tap_blocks(self) -> np.ndarray:
+        """Q8_0 blocks of every quantization site of the most recent forward
+        (the order of sq_ctx_act_tap_read)."""
+        i = self.model.info
+        rows = self._last_rows
+        width = 2 * i.dim + i.n_heads * i.head_dim + i.ffn_dim
+        n = (rows * i.n_layers * width + i.dim) // 32
+        out = np.zeros(n, BLOCK_Q8_0)
+        check(lib().sq_ctx_act_tap_read(self.h, out.ctypes.data, n))
+        return out
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.model.vocab, np.float32)

@@ -101,7 +101,16 @@ int main(int argc, char** argv) {
     const int n_prompt = atoi(argv[4]), n_decode = atoi(argv[5]);
     const unsigned seed = (unsigned)atoi(argv[6]);
     const size_t max_pos = (size_t)atoi(argv[7]);
-    const bool gen = argc > 8 && std::string(argv[8]) == "generate";
+    bool gen = false;
+    // corrupt=<step>,<layer>,<site>,<element>,<kind>: before the lock check of
+    // that step, change one element of the device's blocks by 2 (kind 0) or
+    // one block scale by 1% (kind 1) -- a planted mistake the lock must report
+    int cs = -1, cl = 0, csite = 0, ce = 0, ck = 0;
+    for (int i = 8; i < argc; i++) {
+        const std::string a = argv[i];
+        if (a == "generate") gen = true;
+        if (a.rfind("corrupt=", 0) == 0) sscanf(a.c_str() + 8, "%d,%d,%d,%d,%d", &cs, &cl, &csite, &ce, &ck);
+    }
 
     sq_model* m = nullptr;
     int st = sq_model_load_gguf(path, &m);
@@ -153,6 +162,11 @@ int main(int argc, char** argv) {
     om.layer = layer.data();
     om.inv_freq = inv_freq.data();
     or_ctx* oc = or_ctx_new(&om, max_pos, mode);
+    // the integer path is compared phase-locked: the oracle checks the
+    // device's Q8_0 blocks at every quantization site and continues with them
+    const bool locked = mode != 0 && info.wtype != SQ_BF16 && !(flags & SQ_CTX_F32_ACTS);
+    if (locked && (st = sq_ctx_act_taps(c, 1))) die("sq_ctx_act_taps", st);
+    const size_t TW = 2 * (size_t)info.dim + (size_t)info.n_heads * info.head_dim + info.ffn_dim;
 
     std::vector<float> got(info.vocab);
     for (int step = 0; step <= n_decode; step++) {
@@ -162,7 +176,29 @@ int main(int argc, char** argv) {
         if ((st = sq_logits(c, got.data(), got.size()))) die("sq_logits", st);
         uint32_t tok = 0;
         if ((st = sq_argmax(c, &tok))) die("sq_argmax", st);
-        if ((st = or_forward(&om, oc, p, n))) die("or_forward", st);
+        or_lock lk;
+        memset(&lk, 0, sizeof(lk));
+        std::vector<or_block_q8_0> taps;
+        if (locked) {
+            taps.resize((n * info.n_layers * TW + info.dim) / 32);
+            if ((st = sq_ctx_act_tap_read(c, taps.data(), taps.size()))) die("sq_ctx_act_tap_read", st);
+            if (step == cs) {
+                const size_t site_off[4] = {0, (size_t)info.dim, (size_t)info.dim + info.n_heads * info.head_dim,
+                                            2 * (size_t)info.dim + info.n_heads * info.head_dim};
+                const size_t el = n * (cl * TW + site_off[csite]) + ce;
+                or_block_q8_0& b = taps[el / 32];
+                if (ck == 0) b.qs[el % 32] = (int8_t)(b.qs[el % 32] > 0 ? b.qs[el % 32] - 2 : b.qs[el % 32] + 2);
+                else b.d = or_f32_to_f16(or_f16_to_f32(b.d) * 1.01f);
+            }
+            lk.blocks = taps.data();
+            lk.tol = 0.02f;
+        }
+        if ((st = or_forward_locked(&om, oc, p, n, locked ? &lk : nullptr))) die("or_forward", st);
+        if (locked)
+            printf("lock step %d values %llu flips %llu scale_flips %llu bad %llu first_bad %d/%d/%zu/%.3g\n", step,
+                   (unsigned long long)lk.values, (unsigned long long)lk.flips, (unsigned long long)lk.scale_flips,
+                   (unsigned long long)lk.bad, lk.first_bad_layer, lk.first_bad_site, lk.first_bad_index,
+                   lk.first_bad_dist);
         const float* want = or_ctx_logits(oc);
         double num = 0, den = 0, mx = 0;
         for (uint32_t i = 0; i < info.vocab; i++) {
