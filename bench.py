@@ -1,20 +1,27 @@
 #!/usr/bin/env python3
-"""Benchmark: batch-1 greedy decode of the Llama-3.2-1B-shaped Q8_0 model.
+"""Benchmark: batch-1 prefill + greedy decode of the Llama-3.2-1B-shaped model.
 
-`python bench.py [--gpus 1] [--steps K] [--warmup W] [--config q8|q4|bf16|long|prefill]`
+`python bench.py [--gpus 1] [--steps K] [--warmup W] [--config q8|q4|long|prefill] [--only]`
 
-A step is one decode token (forward + greedy sample) of the token loop,
-timed with HIP events on the context stream; the prompt's prefill is step 0
-and is reported separately as prefill tok/s (the reference's convention:
-decode throughput excludes step 1, scripts/bench.py:68-71).  Weights are
-random-init from a fixed seed (synthetic data; no checkpoint is available).
+The headline is the Q8_0 workload (32-token prompt, then greedy tokens): a
+step is one decode token (forward + greedy sample), timed with HIP events on
+the context stream; the prompt's prefill is step 0 and is reported separately
+as prefill tok/s (the reference's convention: decode throughput excludes step
+1, scripts/bench.py:68-71).  Unless --only is given, the same run then
+measures the other workloads -- Q4_0 (128 + 256), a 4096-position context
+(+128) and a 2048-token batched prefill (+16) -- each in its own block of
+`configs` with its own roofline.  The BF16 workload is reported as not run
+(its kernels are switched off on the device).  Weights are random-init from a
+fixed seed (synthetic data; no checkpoint is available).
 
-One JSON line is printed.  `roofline` prices the dominant kernel against
-MI355X's 8 TB/s HBM peak using its algorithmic bytes and its mean duration
-measured here with HIP events: the persistent decode-step kernel (one launch
-per token), or with --multi-kernel the fused gate/up matvec; `cpu_baseline` is the
-oracle (the C restatement of the reference's x86 scalar path) timed on this
-host over a bounded sample of the same workload.
+One JSON line is printed.  `roofline` prices the decode step (one persistent
+kernel launch per token) against MI355X's 8 TB/s HBM peak using its
+algorithmic bytes and its mean duration measured here with HIP events; the
+prefill block prices its integer matmuls against the 5.0 POP/s int8 and its
+attention against the 157.3 TFLOP/s fp32 matrix-core peaks.
+`cpu_baseline` is the oracle (the C restatement of the reference's x86 scalar
+path) timed on this host, on the reference's thread count (all available
+logical cores), over a bounded sample of the headline workload.
 """
 from __future__ import annotations
 
@@ -33,6 +40,12 @@ import numpy as np  # noqa: E402
 
 METRIC = "decode tok/s batch-1 (1B Q8_0/Q4_0) + % HBM roofline; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0     # dense int8 matrix-core peak
+FP32_MFMA_PEAK_TFLOPS = 157.3
+# Matrix elements per layer of the 1B shape: QKV 2048x3072, o 2048x2048,
+# gate/up 2048x16384, down 8192x2048.
+MATMUL_ELEMS_PER_LAYER = 60817408
+VALU_RESCALE_OPS = 3        # per output element per 32-block in the int8 matmul: cvt, scale product, fma
 CONFIGS = {
     "q8": dict(wtype="Q8_0", prompt=32, gen=64,
                workload="Llama-3.2-1B arch, Q8_0 GGUF, 32-token prompt then 64 greedy tokens"),
@@ -77,12 +90,26 @@ def bytes_per_token(info, P: int) -> int:
             + 2 * L * kvd * 4 + info.vocab * 4)
 
 
+def available_parallelism() -> int:
+    """The thread count the reference's rayon pool takes off macOS
+    (src/cli.rs:37-47,59-62, std::thread::available_parallelism): the CPUs
+    this process may run on, limited by a cgroup CPU quota when one is set."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return max(1, n)
+
+
 def cpu_baseline(path: str, prompt: np.ndarray, n_decode: int, reps: int = 4) -> dict:
     """The oracle's W8A32 decode rate: `reps` runs of the workload's decode
     steps, each after an untimed prefill of the same prompt (about 10 s of
     CPU work at the default workload)."""
     from oracle import oracle as O
-    threads = min(16, os.cpu_count() or 1)
+    threads = available_parallelism()
     O.set_threads(threads)
     m = O.OracleModel(path)
     dt = 0.0
@@ -97,9 +124,11 @@ def cpu_baseline(path: str, prompt: np.ndarray, n_decode: int, reps: int = 4) ->
         dt += time.perf_counter() - t0
         c.close()
     return {"value": round(reps * n_decode / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "nproc": os.cpu_count(),
             "sample": f"{reps} x ({len(prompt)}-token prefill, untimed, then {n_decode} timed decode steps) "
                       f"of the same GGUF; C restatement of the reference's x86 scalar-fallback path "
-                      f"(f32 activations, W8A32), {threads} threads"}
+                      f"(f32 activations, W8A32), {threads} threads = the available parallelism of this "
+                      f"process ({os.cpu_count()} logical CPUs on the host)"}
 
 
 def copy_calibration(mib: int) -> int:
@@ -116,28 +145,123 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def source_digest(*names: str) -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for n in names:
+        with open(os.path.join(REPO, "squirrel-rs_amd", "csrc", n), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(kernel: str, config: str):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by the copy calibration),
-    or None when no measurement exists for this kernel and workload."""
+    with the digest of the kernel source it was measured on: (bytes, None),
+    or (None, reason) when there is no measurement for this kernel and
+    workload or the source has changed since."""
     path = os.path.join(REPO, "profiles", f"traffic_{kernel}_{config}.json")
     try:
         with open(path) as f:
-            return int(json.load(f)["traffic_bytes_per_launch"])
+            rec = json.load(f)
+        b = int(rec["traffic_bytes_per_launch"])
     except (OSError, ValueError, KeyError):
-        return None
+        return None, "no counter measurement for this kernel and workload"
+    want = rec.get("source_digest")
+    have = source_digest(*rec.get("source_files", ["k_step.hip"]))
+    if want != have:
+        return None, f"counter measurement is stale (kernel source {have}, measured on {want})"
+    return b, None
+
+
+def run_workload(name: str, cfg: dict, K: int, W: int, seed: int, kernel_iters: int, multi_kernel: bool) -> dict:
+    """One workload: prefill + K timed decode steps (after W warmup steps);
+    returns its block of the JSON line."""
+    import sqhip
+    path = model_path(cfg["wtype"], seed)
+    t0 = time.time()
+    model = sqhip.Llama3_2(path)
+    info = model.info
+    log(f"[{name}] loaded {path} ({info.weight_bytes / 1e6:.1f} MB of matrices) in {time.time() - t0:.1f}s")
+    S = cfg["prompt"]
+    prompt = np.random.default_rng(seed).integers(0, info.vocab, S).astype(np.uint32)
+    ctx = model.new_context(S + max(K, W) + 2, persistent=not multi_kernel)
+    gen = sqhip.TextTokenGenerator(model, ctx)
+    if W > 0:
+        gen.generate(prompt, W + 1, ignore_eos=True)
+    sqhip.check(sqhip.lib().sq_synchronize())
+    wall0 = time.perf_counter()
+    toks, ms = gen.generate(prompt, K + 1, ignore_eos=True)
+    sqhip.check(sqhip.lib().sq_synchronize())
+    wall = time.perf_counter() - wall0
+    assert len(toks) == K + 1, "generation stopped early"
+    prefill_ms = float(ms[0])
+    decode_ms = float(np.sum(ms[1:K + 1]))
+    tok_s = K / (decode_ms / 1e3)
+    log(f"[{name}] prefill {S} tokens: {prefill_ms:.2f} ms; decode {K} steps: {decode_ms:.2f} ms "
+        f"({tok_s:.1f} tok/s); wall {wall * 1e3:.1f} ms")
+    avg_bytes = float(np.mean([bytes_per_token(info, S + k) for k in range(1, K + 1)]))
+    step_gbs = avg_bytes / (decode_ms / K / 1e3) / 1e9
+    block = {
+        "workload": cfg["workload"], "weights": cfg["wtype"], "prompt_tokens": S, "decode_steps": K,
+        "generated_tokens": K + 1, "positions_attended": [S + 1, S + K],
+        "decode_tok_s": round(tok_s, 2), "ms_per_step": round(decode_ms / K, 4),
+        "prefill_tok_s": round(S / (prefill_ms / 1e3), 1), "prefill_ms": round(prefill_ms, 3),
+        "decode_kernel": "persistent decode step" if ctx.persistent else "one kernel per op (hipGraph)",
+    }
+    traffic, why = measured_traffic("decode_step", name) if ctx.persistent else (None, "multi-kernel path")
+    block["roofline"] = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "bytes_per_launch": int(avg_bytes)}
+    if why:
+        block["roofline"]["traffic_note"] = why
+    if name == "prefill":
+        ph = ctx.prefill_phases(prompt)
+        L = info.n_layers
+        mm_ops = 2.0 * S * MATMUL_ELEMS_PER_LAYER * L
+        attn_flops = 4.0 * info.head_dim * S * (S + 1) / 2 * info.n_heads * L
+        mm_tops = mm_ops / (ph["matmul"] / 1e3) / 1e12
+        at_tflops = attn_flops / (ph["attention"] / 1e3) / 1e12
+        # VALU ceiling of the int8 matmul's per-block rescale: 256 CUs x 64
+        # lanes x 2.4 GHz element operations, VALU_RESCALE_OPS per 64 int8 ops
+        valu_ceiling = 256 * 64 * 2.4e9 / VALU_RESCALE_OPS * 64 / 1e12
+        block["prefill_phases_ms"] = {k: round(v, 3) for k, v in ph.items()}
+        block["prefill_mfma"] = {
+            "matmul_int8_tops": round(mm_tops, 1), "matmul_frac_of_int8_peak": round(mm_tops / INT8_PEAK_TOPS, 4),
+            "matmul_valu_rescale_ceiling_tops": round(valu_ceiling, 1),
+            "matmul_frac_of_rescale_ceiling": round(mm_tops / valu_ceiling, 4),
+            "attention_tflops": round(at_tflops, 1),
+            "attention_frac_of_fp32_mfma_peak": round(at_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "matmul_ops": mm_ops, "attention_flops": attn_flops}
+        block["prefill_roofline"] = {"bound": "mfma", "achieved": round(mm_tops, 1), "peak": INT8_PEAK_TOPS,
+                                     "unit": "TOP/s", "frac": round(mm_tops / INT8_PEAK_TOPS, 4),
+                                     "kernel": "gemm_mfma_kernel (int8 v_mfma_i32_16x16x32_i8)"}
+        log(f"[{name}] prefill phases {ph}; int8 matmul {mm_tops:.0f} TOP/s, attention {at_tflops:.1f} TFLOP/s")
+    if kernel_iters and name == "q8":
+        kernels = {}
+        for which, kname in KERNELS.items():
+            us, nbytes = ctx.time_kernel(which, kernel_iters)
+            kernels[kname] = {"mean_us": round(us, 3), "bytes": int(nbytes), "gbs": round(nbytes / us / 1e3, 1)}
+        block["multi_kernel_path_kernels"] = kernels
+    block["_info"] = info
+    block["_path"] = path
+    block["_prompt"] = prompt
+    ctx.close()
+    model.close()
+    return block
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="decode steps timed")
+    ap.add_argument("--steps", type=int, default=None, help="decode steps timed (headline workload)")
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--config", default="q8", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="q8", choices=sorted(CONFIGS), help="the headline workload")
+    ap.add_argument("--only", action="store_true", help="measure the headline workload only")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=None,
-                    help="decode steps timed on the CPU (default: the same count as the GPU run)")
+                    help="decode steps timed on the CPU (default: the same count as the GPU run, at most 64)")
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--multi-kernel", action="store_true",
                     help="decode with one kernel per op (hipGraph) instead of the persistent step kernel")
@@ -152,60 +276,28 @@ def main() -> int:
 
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.config == "bf16":
+        print("the BF16 workload's kernels (f32 activations) are switched off on the device", file=sys.stderr)
+        return 2
 
-    import sqhip
     cfg = CONFIGS[args.config]
     K = args.steps if args.steps is not None else cfg["gen"] - 1
     W = args.warmup
-    path = model_path(cfg["wtype"], args.seed)
-    t0 = time.time()
-    model = sqhip.Llama3_2(path)
-    info = model.info
-    log(f"loaded {path} ({info.weight_bytes / 1e6:.1f} MB of matrices) in {time.time() - t0:.1f}s")
-    S = cfg["prompt"]
-    prompt = np.random.default_rng(args.seed).integers(0, info.vocab, S).astype(np.uint32)
-    ctx = model.new_context(S + max(K, W) + 2, persistent=not args.multi_kernel)
-    gen = sqhip.TextTokenGenerator(model, ctx)
+    head = run_workload(args.config, cfg, K, W, args.seed, args.kernel_iters, args.multi_kernel)
+    info, path, prompt = head.pop("_info"), head.pop("_path"), head.pop("_prompt")
 
-    if W > 0:
-        gen.generate(prompt, W + 1, ignore_eos=True)
-        log(f"warmup: {W} decode steps")
-    sqhip.check(sqhip.lib().sq_synchronize())
-    wall0 = time.perf_counter()
-    toks, ms = gen.generate(prompt, K + 1, ignore_eos=True)
-    sqhip.check(sqhip.lib().sq_synchronize())
-    wall = time.perf_counter() - wall0
-    assert len(toks) == K + 1, "generation stopped early"
-    prefill_ms = float(ms[0])
-    decode_ms = float(np.sum(ms[1:K + 1]))
-    tok_s = K / (decode_ms / 1e3)
-    log(f"prefill {S} tokens: {prefill_ms:.2f} ms; decode {K} steps: {decode_ms:.2f} ms "
-        f"({tok_s:.1f} tok/s); wall {wall * 1e3:.1f} ms")
-
-    avg_bytes = np.mean([bytes_per_token(info, S + k) for k in range(1, K + 1)])
-    step_gbs = avg_bytes / (decode_ms / K / 1e3) / 1e9
-
-    kernels = {}
-    for which, name in KERNELS.items():
-        us, nbytes = ctx.time_kernel(which, args.kernel_iters)
-        kernels[name] = {"mean_us": round(us, 3), "bytes": int(nbytes),
-                         "gbs": round(nbytes / us / 1e3, 1)}
-    if ctx.persistent:
-        # The whole decode step is one kernel: its algorithmic bytes per launch
-        # over its mean duration from the HIP events around every step.
-        roofline = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(step_gbs / HBM_PEAK_GBS, 4),
-                    "traffic": measured_traffic("decode_step", args.config),
-                    "kernel": "decode_step_kernel (persistent: one launch per token, all 16 layers + "
-                              "LM head + argmax)",
-                    "bytes_per_launch": int(avg_bytes)}
-    else:
-        dom = kernels["gate_up_matvec"]
-        roofline = {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-                    "traffic": measured_traffic("gate_up_matvec", args.config),
-                    "kernel": "gate_up_matvec (RMSNorm+Q8 prologue, 16384x2048 Q8_0 matvec, "
-                              "SiLU*up+Q8 epilogue)"}
+    configs = {}
+    if not args.only:
+        for name in ("q8", "q4", "long", "prefill"):
+            if name == args.config:
+                continue
+            c = CONFIGS[name]
+            blk = run_workload(name, c, c["gen"] - 1, min(W, 8), args.seed, 0, args.multi_kernel)
+            for k in ("_info", "_path", "_prompt"):
+                blk.pop(k)
+            configs[name] = blk
+        configs["bf16"] = {"workload": CONFIGS["bf16"]["workload"], "status": "not run",
+                           "reason": "the f32-activation kernels (BF16 weights) are switched off on the device"}
 
     cpu = None
     if not args.no_cpu:
@@ -214,19 +306,23 @@ def main() -> int:
         log(f"cpu baseline {cpu['value']} tok/s in {time.time() - t1:.1f}s")
 
     line = {
-        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K,
-        "warmup": W, "ms_per_step": round(decode_ms / K, 4), "higher_is_better": True,
+        "metric": METRIC, "value": head["decode_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": K,
+        "warmup": W, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8" if cfg["wtype"] != "BF16" else "f32",
         "data": "synthetic (seeded random-init weights, random prompt ids)",
-        "config": {"workload": cfg["workload"], "weights": cfg["wtype"], "prompt_tokens": S,
-                   "generated_tokens": K + 1, "batch": 1, "kv_cache": "fp32", "parallelism": "none"},
-        "prefill_tok_s": round(S / (prefill_ms / 1e3), 1),
-        "decode_step_hbm": {"bytes_per_token": int(avg_bytes), "achieved_gbs": round(step_gbs, 1),
-                            "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
-        "roofline": roofline,
+        "config": {"workload": cfg["workload"] if K == cfg["gen"] - 1 else
+                   f"{cfg['workload'].split(' then ')[0]} then {K + 1} greedy tokens",
+                   "weights": cfg["wtype"], "prompt_tokens": cfg["prompt"], "generated_tokens": K + 1,
+                   "positions_attended": head["positions_attended"], "batch": 1, "kv_cache": "fp32",
+                   "parallelism": "none"},
+        "prefill_tok_s": head["prefill_tok_s"],
+        "roofline": dict(head["roofline"], kernel="decode_step_kernel (persistent: one launch per token, all "
+                         "layers + LM head + argmax)"),
         "cpu_baseline": cpu,
-        "kernels": kernels,
+        "configs": configs,
     }
+    if "multi_kernel_path_kernels" in head:
+        line["multi_kernel_path_kernels"] = head["multi_kernel_path_kernels"]
     print(json.dumps(line), flush=True)
     return 0
 

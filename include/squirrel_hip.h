@@ -250,6 +250,14 @@ int sq_softmax(const float* d_in, float* d_out, size_t n);
  * write the KV row at the current position); the replays write the same
  * buffers the step does, so reset or re-prefill the context afterwards. */
 int sq_ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes);
+/* Phase split of a batched prefill (measurement aid, no reference
+ * counterpart): resets the context, prefills ids (n >= 2) with HIP events
+ * between launch groups, and returns in ms[0..3] the milliseconds spent in the
+ * integer matmuls (matrix cores, including a K split's sum), in the causal
+ * attention, in everything else (embedding, norms, quantization, RoPE,
+ * SiLU, LM head, argmax), and in the whole prefill.  The context holds the
+ * prompt afterwards, as after sq_forward. */
+int sq_ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms);
 
 #ifdef __cplusplus
 }

@@ -739,7 +739,10 @@ __device__ __forceinline__ ActQ xw_block(const unsigned* xw, int nblk, int blk) 
 // Lanes with `valid` false hold no element (their half is not published).
 // The block maxima and the byte packing move values between lanes with DPP
 // and lane reads only: LDS permutes would queue behind the ring traffic.
-__device__ __forceinline__ void quant_put(float v, int lane, int block0, u64* q, u64* s, unsigned tag, bool valid) {
+// When tq is non-null the blocks also go to the activation taps: payload
+// word i to tq[i], the fp16 scale of block b to td[b].
+__device__ __forceinline__ void quant_put(float v, int lane, int block0, u64* q, u64* s, unsigned tag, bool valid,
+                                          int* tq = nullptr, uint16_t* td = nullptr) {
     float m = fabsf(valid ? v : 0.0f);
     m = fmaxf(m, dpp_mov<0xB1, 0xF>(m));   // quad_perm [1,0,3,2]
     m = fmaxf(m, dpp_mov<0x4E, 0xF>(m));   // quad_perm [2,3,0,1]
@@ -757,9 +760,16 @@ __device__ __forceinline__ void quant_put(float v, int lane, int block0, u64* q,
     // bytes of lanes 4k+1, 4k+2, 4k+3 to lane 4k: quad_perm [1,1,1,1], [2,2,2,2], [3,3,3,3]
     const int b1 = dpp_int<0x55>(qv), b2 = dpp_int<0xAA>(qv), b3 = dpp_int<0xFF>(qv);
     const int blk = block0 + (lane >> 5);
-    if ((lane & 3) == 0 && valid)
-        put(q + (size_t)blk * 8 + ((lane & 31) >> 2), (unsigned)(qv | (b1 << 8) | (b2 << 16) | (b3 << 24)), tag);
-    if ((lane & 31) == 0 && valid) putf(s + blk, sq_f16_to_f32(sq_f32_to_f16(sc)), tag);
+    const unsigned word = (unsigned)(qv | (b1 << 8) | (b2 << 16) | (b3 << 24));
+    const uint16_t d16 = sq_f32_to_f16(sc);
+    if ((lane & 3) == 0 && valid) {
+        put(q + (size_t)blk * 8 + ((lane & 31) >> 2), word, tag);
+        if (tq) gl(tq)[(size_t)blk * 8 + ((lane & 31) >> 2)] = (int)word;
+    }
+    if ((lane & 31) == 0 && valid) {
+        putf(s + blk, sq_f16_to_f32(d16), tag);
+        if (tq) gl(td)[blk] = d16;
+    }
 }
 
 __device__ __forceinline__ void arg_merge(float& bv, int& bi, int& bn, float v, int i, int n) {
@@ -860,7 +870,21 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     // quantized-activation taps (sq_ctx::tap_q layout): per layer, sites of
     // width D, QD, D, F
     const size_t TW = 2 * (size_t)D + QD + F;
-    const bool tapping = a.taps != 0 && wg == 0;
+    const bool tap_a = a.taps != 0;               // producers write their blocks' taps
+    const bool tapping = tap_a && wg == 0;        // workgroup 0 writes the norm sites' taps
+    // Tap addresses of site offset `so` of layer l, formed where they are used:
+    // the opaque offset keeps the compiler from holding one address per site
+    // live across the layer loop (register pressure).
+    auto tap_q = [&](int l, size_t so) -> int8_t* {
+        size_t o = (size_t)l * TW + so;
+        asm volatile("" : "+s"(o));
+        return a.dbg_qs + o;
+    };
+    auto tap_d = [&](int l, size_t so) -> uint16_t* {
+        size_t o = ((size_t)l * TW + so) / 32;
+        asm volatile("" : "+s"(o));
+        return a.dbg_d + o;
+    };
     int gen = 0;  // compute-group barrier count
     auto next_xw = [&]() -> unsigned* { return S.xw; };
 
@@ -974,8 +998,8 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 const bool tap0 = wg == 0 && (l == 0 || tapping);
                 stamp(l, TS_QKV_POLL);
                 if (!norm_quant(S, l == 0 ? nullptr : X.h, l == 0 ? 0u : tag(l - 1, PH_DOWN), embed_at, gn, D, a.eps,
-                                (l == 0 && wg == 0) ? a.dbg_normed : nullptr, tap0 ? a.dbg_qs + l * TW : nullptr,
-                                tap0 ? a.dbg_d + l * TW / 32 : nullptr, gen, C))
+                                (l == 0 && wg == 0) ? a.dbg_normed : nullptr, tap0 ? tap_q(l, 0) : nullptr,
+                                tap0 ? tap_d(l, 0) : nullptr, gen, C))
                     return;
                 stamp(l, TS_QKV_IN);
                 const ActQ A = act_lane(S, D);
@@ -1150,7 +1174,8 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 for (int tile = t_begin; tile + 1 < t_end; tile++) do_tile(tile, std::false_type{});
                 do_tile(t_end - 1, std::true_type{});
                 if (nchunks == 1) {
-                    quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, T, true);
+                    quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, T, true, tap_a ? (int*)tap_q(l, D) : nullptr,
+                              tap_a ? tap_d(l, D) : nullptr);
                 } else {
                     // partial (o[64], m, l) of head h, chunk `chunk`
                     u64* pt = X.t + ((size_t)h * a.max_tiles + chunk) * (HDIM + 2);
@@ -1210,7 +1235,9 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                             ok = merge_batch(t0, std::integral_constant<int, 8>{});
                     }
                     // lanes of one wavefront agree on ok (any failure aborts)
-                    if (__all(ok)) quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, Tm, true);
+                    if (__all(ok))
+                        quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, Tm, true,
+                                  tap_a ? (int*)tap_q(l, D) : nullptr, tap_a ? tap_d(l, D) : nullptr);
                     else ok = false;
                 }
                 if (!ok) return fail();
@@ -1226,12 +1253,6 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 unsigned* xw = next_xw();
                 if (!gather(S, xw, X.a, QD / 4 + QB, Tin, C, gen)) return;
                 stamp(l, TS_O_IN);
-                if (tapping) {  // the attention output's blocks
-                    const gptr<int> tq = (gptr<int>)gl(a.dbg_qs + l * TW + D);
-                    const gptr<uint16_t> td = gl(a.dbg_d + (l * TW + D) / 32);
-                    for (int i = tid; i < QD / 4; i += CNT) tq[i] = (int)xw[i];
-                    for (int i = tid; i < QB; i += CNT) td[i] = sq_f32_to_f16(__builtin_bit_cast(float, xw[QD / 4 + i]));
-                }
                 if (n_own > 0) {
                     const ActQ A = xw_block<WT>(xw, QB, lane);
                     float res[RMAX];
@@ -1259,8 +1280,7 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 const Gains gn = load_gains(LY[l].ffn_norm, D);
                 const long long rw0 = ring_wait;
                 if (!norm_quant(S, X.h, tag(l, PH_O), embed_at, gn, D, a.eps, nullptr,
-                                tapping ? a.dbg_qs + l * TW + D + QD : nullptr,
-                                tapping ? a.dbg_d + (l * TW + D + QD) / 32 : nullptr, gen, C))
+                                tapping ? tap_q(l, D + QD) : nullptr, tapping ? tap_d(l, D + QD) : nullptr, gen, C))
                     return;
                 stamp(l, TS_GU_IN);
                 const ActQ A = act_lane(S, D);
@@ -1290,7 +1310,8 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                     const float gt = S.gu[j];
                     const float up = S.gu[32 + j];
                     const float f = (gt * sq_sigmoid(gt)) * up;
-                    quant_put(f, lane, g.tile, X.f, X.f + F / 4, T, lane < 32);
+                    quant_put(f, lane, g.tile, X.f, X.f + F / 4, T, lane < 32,
+                              tap_a ? (int*)tap_q(l, 2 * D + QD) : nullptr, tap_a ? tap_d(l, 2 * D + QD) : nullptr);
                 }
             }
             consumed(lb + g.offd);
@@ -1309,12 +1330,6 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                 unsigned* xw = next_xw();
                 if (!gather(S, xw, X.f, F / 4 + FB, tag(l, PH_GU), C, gen)) return;
                 stamp(l, TS_DOWN_IN);
-                if (tapping) {  // the FFN activation's blocks
-                    const gptr<int> tq = (gptr<int>)gl(a.dbg_qs + l * TW + 2 * D + QD);
-                    const gptr<uint16_t> td = gl(a.dbg_d + (l * TW + 2 * D + QD) / 32);
-                    for (int i = tid; i < F / 4; i += CNT) tq[i] = (int)xw[i];
-                    for (int i = tid; i < FB; i += CNT) td[i] = sq_f32_to_f16(__builtin_bit_cast(float, xw[F / 4 + i]));
-                }
                 if (n_own > 0) {
                     const int pu = stream_row_units(WT, F) - F / 256;
                     if (!ensure(lb + g.offd + (cw + NCW * (n_own - 1) + 1) * g.ud)) return fail();

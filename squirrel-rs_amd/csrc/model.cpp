@@ -616,6 +616,18 @@ int run_prefill(sq_ctx* c, size_t n) {
         SQ_HIP_CHECK(hipMemcpyAsync(c->ptap_d + off / 32, c->p_ad, n * k / 16, hipMemcpyDeviceToDevice, s));
         return 0;
     };
+    // phase boundary for the measurement entry point (kind: 0 matmul,
+    // 1 attention, 2 other, 3 end)
+    auto phase = [&](int kind) -> int {
+        if (!c->prof) return 0;
+        hipEvent_t e;
+        SQ_HIP_CHECK(hipEventCreate(&e));
+        c->prof_ev.push_back(e);
+        c->prof_kind.push_back(kind);
+        SQ_HIP_CHECK(hipEventRecord(e, s));
+        return 0;
+    };
+    if ((st = phase(2))) return st;
     SQ_HIP_CHECK(hipMemcpyAsync(c->d_ids, c->h_pinned, n * 4, hipMemcpyHostToDevice, s));
     if ((st = launch_embed(s, view(m->embd), m->wtype, c->d_ids, (int)n, D, c->p_hidden))) return st;
     const int pos0 = (int)c->seq_len;
@@ -629,34 +641,46 @@ int run_prefill(sq_ctx* c, size_t n) {
                                       a8 ? c->p_aq : nullptr, c->p_ad)) ||
             (st = tap(l, 0, D)))
             return st;
-        if ((st = launch_gemm(s, view(L.qkv), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_qkv,
-                              QD + 2 * KVD, false, c->p_split, kGemmSplitFloats)))
+        if ((st = phase(0)) ||
+            (st = launch_gemm(s, view(L.qkv), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_qkv,
+                              QD + 2 * KVD, false, c->p_split, kGemmSplitFloats)) ||
+            (st = phase(2)))
             return st;
         if ((st = launch_rope_kv_rows(s, c->p_qkv, QD + 2 * KVD, N, QD, KVD, hd, pos0, c->rope, c->p_q, kc, vc)))
             return st;
-        if ((st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd, c->p_attn))) return st;
+        if ((st = phase(1)) ||
+            (st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd, c->p_attn)) ||
+            (st = phase(2)))
+            return st;
         if (a8 && ((st = launch_quantize_rows(s, c->p_attn, (size_t)N * QD, c->p_aq, c->p_ad)) || (st = tap(l, 1, QD))))
             return st;
-        if ((st = launch_gemm(s, view(L.o), m->wtype, a8, c->p_aq, c->p_ad, c->p_attn, N, c->p_hidden, D, true,
-                              c->p_split, kGemmSplitFloats)))
+        if ((st = phase(0)) ||
+            (st = launch_gemm(s, view(L.o), m->wtype, a8, c->p_aq, c->p_ad, c->p_attn, N, c->p_hidden, D, true,
+                              c->p_split, kGemmSplitFloats)) ||
+            (st = phase(2)))
             return st;
         if ((st = launch_rmsnorm_rows(s, c->p_hidden, L.ffn_norm, N, D, g.eps, a8 ? nullptr : c->p_normed,
                                       a8 ? c->p_aq : nullptr, c->p_ad)) ||
             (st = tap(l, 2, D)))
             return st;
-        if ((st = launch_gemm(s, view(L.gateup), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_gu, 2 * F,
-                              false, c->p_split, kGemmSplitFloats)))
+        if ((st = phase(0)) ||
+            (st = launch_gemm(s, view(L.gateup), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_gu, 2 * F,
+                              false, c->p_split, kGemmSplitFloats)) ||
+            (st = phase(2)))
             return st;
         if ((st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, c->p_act, a8 ? c->p_aq : nullptr, c->p_ad)) ||
             (a8 && (st = tap(l, 3, F))))
             return st;
-        if ((st = launch_gemm(s, view(L.down), m->wtype, a8, c->p_aq, c->p_ad, c->p_act, N, c->p_hidden, D, true,
-                              c->p_split, kGemmSplitFloats)))
+        if ((st = phase(0)) ||
+            (st = launch_gemm(s, view(L.down), m->wtype, a8, c->p_aq, c->p_ad, c->p_act, N, c->p_hidden, D, true,
+                              c->p_split, kGemmSplitFloats)) ||
+            (st = phase(2)))
             return st;
     }
     SQ_HIP_CHECK(hipMemcpyAsync(c->hidden, c->p_hidden + (size_t)(N - 1) * D, (size_t)D * 4,
                                 hipMemcpyDeviceToDevice, s));
-    return run_head(c, N);
+    if ((st = run_head(c, N))) return st;
+    return phase(3);
 }
 
 }  // namespace
@@ -880,6 +904,30 @@ int ctx_forward(sq_ctx* c, const uint32_t* ids, size_t n) {
     c->seq_len += n;
     c->last_rows = n;
     c->last_tapped = c->a8 && (n > 1 ? c->taps : (c->taps || !c->persist));
+    return 0;
+}
+
+int ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms) {
+    if (n < 2) return set_error(SQ_ERR_ARG, "prefill_phases: needs a prompt of at least 2 tokens");
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    c->seq_len = 0;
+    SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
+    c->prof = true;
+    int st = ctx_forward(c, ids, n);
+    c->prof = false;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    for (int k = 0; k < 4; k++) ms[k] = 0.0;
+    for (size_t i = 0; !st && e == hipSuccess && i + 1 < c->prof_ev.size(); i++) {
+        float t = 0.f;
+        e = hipEventElapsedTime(&t, c->prof_ev[i], c->prof_ev[i + 1]);
+        ms[c->prof_kind[i]] += t;
+        ms[3] += t;
+    }
+    for (hipEvent_t ev : c->prof_ev) (void)hipEventDestroy(ev);
+    c->prof_ev.clear();
+    c->prof_kind.clear();
+    if (st) return st;
+    if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("prefill_phases: ") + hipGetErrorString(e));
     return 0;
 }
 

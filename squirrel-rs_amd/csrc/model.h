@@ -134,6 +134,12 @@ struct sq_ctx {
     hipGraphExec_t graph = nullptr;
     hipGraph_t graph_def = nullptr;
 
+    // Prefill phase timing (measurement only): events recorded between
+    // launch groups, each interval charged to the kind of its first launch.
+    bool prof = false;
+    std::vector<hipEvent_t> prof_ev;
+    std::vector<int> prof_kind;
+
     // Per-kernel relaunchers of the decode step (measurement only).
     std::vector<std::function<int()>> kernels;
     std::vector<uint64_t> kernel_bytes;
@@ -163,6 +169,9 @@ int ctx_generate(sq_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t max_
                  uint32_t* out, size_t* n_out, double* step_ms);
 int ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes);
 int ctx_set_taps(sq_ctx* c, bool on);
+// Runs a prefill of ids on a reset context with HIP events between launch
+// groups; ms[0..3] = int8 matmuls, attention, everything else, whole prefill.
+int ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms);
 // Host copy of the most recent forward's quantized activations as GGUF
 // Q8_0 blocks: per layer, per site, rows x k/32 blocks; then the LM-head row.
 int ctx_read_taps(sq_ctx* c, void* blocks, size_t n_blocks);

@@ -179,6 +179,14 @@ class ModelContext:
         check(lib().sq_ctx_time_kernel(self.h, which, iters, C.byref(us), C.byref(b)))
         return us.value, b.value
 
+    def prefill_phases(self, prompt_ids) -> dict:
+        """Milliseconds of one batched prefill by phase (sq_ctx_prefill_phases)."""
+        ids = np.ascontiguousarray(prompt_ids, dtype=np.uint32)
+        ms = np.zeros(4, np.float64)
+        check(lib().sq_ctx_prefill_phases(self.h, ids.ctypes.data, ids.size, ms.ctypes.data))
+        self._last_rows = ids.size
+        return {"matmul": float(ms[0]), "attention": float(ms[1]), "other": float(ms[2]), "total": float(ms[3])}
+
     def close(self) -> None:
         if self.h:
             lib().sq_ctx_free(self.h)
