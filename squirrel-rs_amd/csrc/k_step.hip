@@ -1603,6 +1603,8 @@ int launch_build_stream(hipStream_t s, int wtype, const StepArgs& a, int grid, v
     return 0;
 }
 
+static int decode_step_resident(int wtype, int* out);
+
 int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid) {
     if (!decode_step_fits(a.dim, a.ffn, a.n_heads, a.n_kv_heads, grid))
         return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: shape not supported (dim <= 2048, ffn <= 8192, "
@@ -1610,9 +1612,18 @@ int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid) {
     if (a.stream == nullptr ||
         a.stream_stride != decode_stream_stride(wtype, a.n_layers, a.dim, a.ffn, a.n_heads, a.n_kv_heads, a.vocab, grid))
         return set_error(SQ_ERR_ARG, "persistent decode step: the weight stream was not built for this grid");
-    // One workgroup per CU (the grid is the CU count and a CU holds one of
-    // these workgroups), so every workgroup is resident at once; were one
-    // not, the bounded waits would end the step with an error, not a hang.
+    // The workgroups wait on each other, so all of them must be resident at
+    // once.  A grid above what the device holds (workgroups per CU times the
+    // CU count) is refused here; within it, the launch places one workgroup
+    // per CU.  (A cooperative launch would also guarantee residency against
+    // other work on the device, at about 15 us per token; the bounded waits
+    // end such a step with an error instead of a hang.)
+    int resident = 0;
+    if (int st = decode_step_resident(wtype, &resident)) return st;
+    if (grid > resident)
+        return set_error(SQ_ERR_HIP, "decode step launch: a grid of " + std::to_string(grid) +
+                                         " workgroups cannot be resident at once on this device (at most " +
+                                         std::to_string(resident) + ")");
     if (wtype == WT_Q8_0)
         hipLaunchKernelGGL(decode_step_kernel<WT_Q8_0>, dim3(grid), dim3(SNT), 0, s, a);
     else if (wtype == WT_Q4_0)
@@ -1624,13 +1635,31 @@ int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid) {
     return 0;
 }
 
+// Workgroups of the step kernel the current device holds at once (per CU
+// times CUs), looked up once per device.
+static int decode_step_resident(int wtype, int* out) {
+    static int cached[2][64] = {};
+    int dev = 0;
+    SQ_HIP_CHECK(hipGetDevice(&dev));
+    int& slot = cached[wtype == WT_Q4_0 ? 1 : 0][dev & 63];
+    if (slot == 0) {
+        int cus = 0, per_cu = 0;
+        SQ_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        const void* f =
+            wtype == WT_Q4_0 ? (const void*)decode_step_kernel<WT_Q4_0> : (const void*)decode_step_kernel<WT_Q8_0>;
+        SQ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, SNT, 0));
+        slot = per_cu * cus;
+    }
+    *out = slot;
+    return 0;
+}
+
 int decode_step_max_grid(int wtype, int* grid) {
-    int dev = 0, cus = 0, per_cu = 0;
+    int dev = 0, cus = 0, resident = 0;
     SQ_HIP_CHECK(hipGetDevice(&dev));
     SQ_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    const void* f = wtype == WT_Q4_0 ? (const void*)decode_step_kernel<WT_Q4_0> : (const void*)decode_step_kernel<WT_Q8_0>;
-    SQ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, SNT, 0));
-    if (per_cu < 1) return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step does not fit on a CU");
+    if (int st = decode_step_resident(wtype, &resident)) return st;
+    if (resident < cus) return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step does not fit on a CU");
     *grid = cus;
     return 0;
 }

@@ -696,12 +696,13 @@ int setup_persistent(sq_ctx* c) {
         return 0;
     int grid = 0, st;
     if ((st = decode_step_max_grid(m->wtype, &grid))) return st;
-    // SQUIRREL_STEP_GRID caps the CUs the kernel occupies (to leave CUs to
-    // other work on the device); a cap the shape does not fit in selects the
-    // multi-kernel path.
+    // SQUIRREL_STEP_GRID sets the workgroup count (one per CU by default):
+    // below the CU count it leaves CUs to other work on the device; a count
+    // the shape does not fit in selects the multi-kernel path; a count above
+    // what the device holds at once is refused at launch.
     if (const char* e = getenv("SQUIRREL_STEP_GRID")) {
-        const int cap = atoi(e);
-        if (cap > 0 && cap < grid) grid = cap;
+        const int req = atoi(e);
+        if (req > 0) grid = req;
     }
     if (!decode_step_fits(g.dim, g.ffn, g.n_heads, g.n_kv_heads, grid)) return 0;
     const int QD = g.n_heads * g.head_dim, KVD = g.n_kv_heads * g.head_dim;

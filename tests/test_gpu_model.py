@@ -205,6 +205,25 @@ def test_long_prefill_unsplit_matrix_core_tiles(tiny_gguf, wtype):
         assert t == O.greedy(g)
 
 
+def test_persistent_grid_beyond_residency_is_refused(tiny_gguf, monkeypatch):
+    """The persistent step's workgroups wait on each other: a grid the device
+    cannot hold at once (SQUIRREL_STEP_GRID far above the CU count, one
+    workgroup per CU) is refused at launch, without waiting for the bounded
+    in-kernel time-outs."""
+    import time
+    monkeypatch.setenv("SQUIRREL_STEP_GRID", "768")
+    m = sq.Llama3_2(tiny_gguf("Q8_0", "g4"))
+    c = m.new_context(64)
+    assert c.persistent
+    c.forward(np.arange(1, 6, dtype=np.uint32))  # the prefill does not use the step kernel
+    t0 = time.perf_counter()
+    with pytest.raises(sq.SqError) as e:
+        c.forward([7])
+        c.logits()
+    assert "cannot be resident" in str(e.value)
+    assert time.perf_counter() - t0 < 0.2
+
+
 def test_persistent_deterministic_across_resets(tiny_gguf):
     """Back-to-back generations, with and without a reset in between, give
     the same tokens and logits (barrier epochs carry over between launches)."""
