@@ -21,6 +21,9 @@ ARCH = "gfx950"
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
+# Per-file additions.  The prefill matmul converts every MFMA result on the
+# VALU, so its results are placed straight in VGPRs (no AGPR copy-out).
+FILE_FLAGS = {"k_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 CXX_FLAGS = ["-x", "c++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
              "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
 
@@ -40,7 +43,7 @@ def host_cxx() -> str:
 def _compile(src: str) -> tuple[str, str, int]:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
     if src.endswith(".hip"):
-        cmd = [hipcc(), *HIP_FLAGS, "-c", src, "-o", obj]
+        cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     else:
         cmd = [host_cxx(), *CXX_FLAGS, "-c", src, "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)

@@ -181,6 +181,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_kernel(MatView w, const int8_
 // 32-element block, which is one v_mfma_i32_16x16x32_i8 (K = 32) for a
 // 16 x 16 tile of outputs.
 //
+// The kernel is bound by VALU issue: each output element and block costs
+// the conversion of isum and the fused add.  The scale product sa * sw of
+// two f16 values has at most 22 significant bits, so it is exact in f32
+// however it is formed; it comes from one v_mfma_f32_16x16x16_f16 per tile
+// and block, already in the result layout: lanes 0-15 hold the row's four
+// block scales in k-slots 0-3 (the other lanes zeros), and the column
+// operand of block b holds sw_b in k-slot b and zeros elsewhere.
+//
 // A workgroup computes a 64 x 64 tile of (activation rows) x (weight rows)
 // with four wavefronts of 32 x 32 (2 x 2 MFMA tiles).  K advances in chunks
 // of four blocks: the chunk's activation and weight bytes (64 rows x 128 B
@@ -196,6 +204,7 @@ constexpr int MQ_LD = MQ_KC + 8;   // LDS row stride in bytes
 
 typedef int mq_v4i __attribute__((ext_vector_type(4)));
 typedef float sq_v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 mq_v4h __attribute__((ext_vector_type(4)));
 
 template <int WT>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t* __restrict__ aq,
@@ -204,8 +213,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
                                                         int kbs, size_t split_stride) {
     __shared__ __attribute__((aligned(16))) int8_t sA[MQ_T * MQ_LD];
     __shared__ __attribute__((aligned(16))) int8_t sW[MQ_T * MQ_LD];
-    __shared__ __attribute__((aligned(16))) float sSa[MQ_T][MQ_KB];
-    __shared__ __attribute__((aligned(16))) float sSw[MQ_T][MQ_KB];
+    // f16 block scales: sSa[row][b]; row MQ_T is zeros (the k-slots of
+    // lanes 16-63).  sSw[b][col] holds sw_b in slot b, zeros elsewhere
+    // (16 lanes read 16 consecutive columns of one block).
+    __shared__ __attribute__((aligned(16))) uint16_t sSa[MQ_T + 1][MQ_KB];
+    __shared__ __attribute__((aligned(16))) uint16_t sSw[MQ_KB][MQ_T][MQ_KB];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = w.k, KB = K >> 5;
@@ -227,8 +239,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
 
     // This thread's share of a chunk: activation (and Q8_0 weight) pieces
     // tid and tid + 256 of 64 rows x 8 sixteen-byte pieces, or one packed
-    // Q4_0 block (row tid / 4, block tid % 4); the scales of row tid / 4,
-    // block tid % 4.  The next chunk's share is loaded into registers while
+    // Q4_0 block (row tid / 4, block tid % 4); the scales of row tid % 64,
+    // block tid / 64.  The next chunk's share is loaded into registers while
     // the current one is multiplied.
     sq_v4i ra[2], rw[2];
     uint16_t rsa, rsw;
@@ -244,11 +256,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
                 if (n0 + r < w.rows && k < kb_end * 32) rw[q] = *(const sq_v4i*)((const int8_t*)w.qs + (size_t)(n0 + r) * K + k);
             }
         }
-        const int r = tid >> 2, kb = kb0 + (tid & 3);
         if constexpr (WT == WT_Q4_0) {
+            const int r = tid >> 2, kb = kb0 + (tid & 3);
             rw[0] = sq_v4i{(int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888};  // q = 8: zero weights
             if (n0 + r < w.rows && kb < kb_end) rw[0] = *(const sq_v4i*)((const uint8_t*)w.qs + (size_t)(n0 + r) * (K / 2) + kb * 16);
         }
+        const int r = tid & 63, kb = kb0 + (tid >> 6);
         rsa = (m0 + r < m_rows && kb < kb_end) ? ad[(size_t)(m0 + r) * KB + kb] : (uint16_t)0;
         rsw = (n0 + r < w.rows && kb < kb_end) ? w.scale[(size_t)(n0 + r) * KB + kb] : (uint16_t)0;
     };
@@ -266,8 +279,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
                 dw[1] = make_int2(rw[q].z, rw[q].w);
             }
         }
-        const int r = tid >> 2, b = tid & 3;
         if constexpr (WT == WT_Q4_0) {
+            const int r = tid >> 2, b = tid & 3;
             // byte j holds element j (low nibble) and element j + 16 (high
             // nibble); per byte, nibble - 8 as a signed byte: (q | 0x80) - 8
             // stays within the byte, and xor 0x80 restores the sign
@@ -284,46 +297,66 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
             dw[2] = make_int2(hi[0], hi[1]);
             dw[3] = make_int2(hi[2], hi[3]);
         }
-        sSa[r][b] = sq_f16_to_f32(rsa);
-        sSw[r][b] = sq_f16_to_f32(rsw);
+        const int r = tid & 63, b = tid >> 6;
+        sSa[r][b] = rsa;
+        const unsigned sw = (unsigned)rsw << (16 * (b & 1));
+        *(uint2*)&sSw[b][r][0] = (b < 2) ? make_uint2(sw, 0u) : make_uint2(0u, sw);
     };
 
+    if (tid < MQ_KB) sSa[MQ_T][tid] = 0;
     fetch(kb_begin);
     for (int kb0 = kb_begin; kb0 < kb_end; kb0 += MQ_KB) {
         stage();
         __syncthreads();
         if (kb0 + MQ_KB < kb_end) fetch(kb0 + MQ_KB);
-        const int nb = min(MQ_KB, kb_end - kb0);
-        // the chunk's scales of this lane's rows and columns, all four blocks at once
-        sq_v4f sa4[2][4], sw4[2];
+        // the row operands of the scale products: this row's four block
+        // scales on lanes 0-15, zeros on the others
+        mq_v4h sa[2];
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) sa4[i][r] = *(const sq_v4f*)&sSa[wm + 16 * i + (fk >> 1) + r][0];
-#pragma unroll
-        for (int j = 0; j < 2; j++) sw4[j] = *(const sq_v4f*)&sSw[wn + 16 * j + fr][0];
-#pragma unroll
-        for (int b = 0; b < MQ_KB; b++) {
-            if (b >= nb) break;
-            long af[2], bf[2];
+        for (int i = 0; i < 2; i++) sa[i] = *(const mq_v4h*)&sSa[lane < 16 ? wm + 16 * i + fr : MQ_T][0];
+        // Software pipeline over the chunk's blocks: the products of block
+        // b + 1 for tile t are issued as soon as tile t of block b has been
+        // folded in, so the matrix cores run while the VALU converts.  Blocks
+        // past kb_end were staged as zeros (payload and scales), and
+        // fma(0, 0, acc) leaves acc unchanged.
+        long af[2], bf[2];
+        mq_v4h sw[2];
+        auto operands = [&](int b) {
 #pragma unroll
             for (int i = 0; i < 2; i++) af[i] = *(const long*)(sA + (wm + 16 * i + fr) * MQ_LD + 32 * b + fk);
 #pragma unroll
-            for (int j = 0; j < 2; j++) bf[j] = *(const long*)(sW + (wn + 16 * j + fr) * MQ_LD + 32 * b + fk);
+            for (int j = 0; j < 2; j++) {
+                bf[j] = *(const long*)(sW + (wn + 16 * j + fr) * MQ_LD + 32 * b + fk);
+                sw[j] = *(const mq_v4h*)&sSw[b][wn + 16 * j + fr][0];
+            }
+        };
+        const mq_v4i zero = {0, 0, 0, 0};
+        const sq_v4f fzero = {0.0f, 0.0f, 0.0f, 0.0f};
+        mq_v4i d[4];
+        sq_v4f sc[4];
+        operands(0);
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+        for (int t = 0; t < 4; t++) {
+            d[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[t >> 1], bf[t & 1], zero, 0, 0, 0);
+            sc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(sa[t >> 1], sw[t & 1], fzero, 0, 0, 0);
+        }
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const mq_v4i zero = {0, 0, 0, 0};
-                    const mq_v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
+        for (int b = 0; b < MQ_KB; b++) {
+            if (b + 1 < MQ_KB) operands(b + 1);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        // the combine of the reference's aarch64 kernels (dot_prod.rs:189-252):
-                        // acc = fma(f32(isum), sa * sw, acc)
-                        const float sc = sa4[i][r][b] * sw4[j][b];
-                        acc[i][j][r] = fmaf((float)d[r], sc, acc[i][j][r]);
-                    }
+            for (int t = 0; t < 4; t++) {
+                const int i = t >> 1, j = t & 1;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    // the combine of the reference's aarch64 kernels (dot_prod.rs:189-252):
+                    // acc = fma(f32(isum), sa * sw, acc)
+                    acc[i][j][r] = fmaf((float)d[t][r], sc[t][r], acc[i][j][r]);
                 }
+                if (b + 1 < MQ_KB) {
+                    d[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(sa[i], sw[j], fzero, 0, 0, 0);
+                }
+            }
         }
         __syncthreads();
     }

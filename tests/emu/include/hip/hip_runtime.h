@@ -47,10 +47,12 @@ struct alignas(8) float2 { float x, y; };
 struct alignas(16) float4 { float x, y, z, w; };
 struct alignas(8) int2 { int x, y; };
 struct alignas(16) int4 { int x, y, z, w; };
+struct alignas(8) uint2 { unsigned x, y; };
 inline float2 make_float2(float a, float b) { return float2{a, b}; }
 inline float4 make_float4(float a, float b, float c, float d) { return float4{a, b, c, d}; }
 inline int2 make_int2(int a, int b) { return int2{a, b}; }
 inline int4 make_int4(int a, int b, int c, int d) { return int4{a, b, c, d}; }
+inline uint2 make_uint2(unsigned a, unsigned b) { return uint2{a, b}; }
 
 struct dim3 {
     unsigned x, y, z;
@@ -217,6 +219,32 @@ inline sqemu_v4f mfma_f32_16x16x4f32(float a, float b, sqemu_v4f c) {
     }
     return d;
 }
+// v_mfma_f32_16x16x16_f16: lane l supplies A[l%16][4(l/16) .. +3] and
+// B[4(l/16) .. +3][l%16] as four halves.  The sum is formed in double and
+// rounded once, which is the device result whenever that sum is exact in
+// f32 (the only way the kernels use it).
+typedef _Float16 sqemu_v4h __attribute__((ext_vector_type(4)));
+inline sqemu_v4f mfma_f32_16x16x16f16(sqemu_v4h a, sqemu_v4h b, sqemu_v4f c) {
+    uint64_t mine[2];
+    memcpy(&mine[0], &a, 8);
+    memcpy(&mine[1], &b, 8);
+    const uint64_t* all = wave_exchange_n(mine, 2, 0x4002);
+    const int lane = g_lane;
+    const int col = lane & 15;
+    sqemu_v4f d = c;
+    for (int r = 0; r < 4; r++) {
+        const int row = 4 * (lane >> 4) + r;
+        double s = d[r];
+        for (int k = 0; k < 16; k++) {
+            _Float16 av, bv;
+            memcpy(&av, (const char*)&all[2 * (row + 16 * (k >> 2))] + 2 * (k & 3), 2);
+            memcpy(&bv, (const char*)&all[2 * (col + 16 * (k >> 2)) + 1] + 2 * (k & 3), 2);
+            s += (double)av * (double)bv;
+        }
+        d[r] = (float)s;
+    }
+    return d;
+}
 // v_mfma_f32_16x16x8_bf16-style operands are not emulated.
 }  // namespace sqemu
 
@@ -232,6 +260,7 @@ inline sqemu_v4f mfma_f32_16x16x4f32(float a, float b, sqemu_v4f c) {
 #define __builtin_amdgcn_sdot4(a, b, c, cl) ::sqemu::sdot4((a), (b), (c), (cl))
 #define __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, x, y, z) ::sqemu::mfma_i32_16x16x32_i8((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) ::sqemu::mfma_f32_16x16x4f32((a), (b), (c))
+#define __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, x, y, z) ::sqemu::mfma_f32_16x16x16f16((a), (b), (c))
 #define __shfl_xor(v, m, w) ::sqemu::shfl_xor((v), (m), (w))
 
 template <typename T>
