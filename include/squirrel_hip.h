@@ -172,6 +172,15 @@ int sq_ctx_last_hidden(sq_ctx* c, float* out, size_t n);
  * layout).  Lets tests check the fused norm+quantize kernel bit for bit. */
 int sq_ctx_debug_act(sq_ctx* c, float* normed, void* blocks);
 
+/* One window of the perplexity harness (src/bin/perplexity.rs:61-110): on a
+ * reset context, prefill ids[0, burn) (the burn-in), then for every i in
+ * [burn, n) write log p(ids[i]) of the current logits to logp[i - burn]
+ * (f64, as sq_log_softmax_at) and, while i + 1 < n, teacher-force ids[i]
+ * with one decode step.  The whole window is enqueued on the context stream
+ * and the n - burn values come back with one copy.  Needs 1 <= burn < n and
+ * n - 1 <= max_positions; every id below the vocabulary size. */
+int sq_ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* logp);
+
 /* TextTokenGenerator::generate (src/text_generator.rs:38-101) on token ids:
  * prefill `prompt`, then greedy decode until max_tokens tokens or EOS.
  * out_tokens receives the generated ids (max_tokens capacity); step_ms, when
@@ -239,6 +248,11 @@ int sq_elementwise_add(float* d_a, const float* d_b, size_t n);
 int sq_greedy(const float* d_logits, size_t n, uint32_t* token);
 /* softmax_f32 (src/kernels/softmax.rs:4-27) over one row. */
 int sq_softmax(const float* d_in, float* d_out, size_t n);
+/* log_softmax_at (src/bin/perplexity.rs:112-117): log p(idx) under
+ * softmax(d_logits[0..n)) in f64 -- the maximum folded in f32, the sum of
+ * exp(l - max) in f64 (a fixed-order tree rather than a sequential fold).
+ * idx >= n is SQ_ERR_ARG (the reference would panic on the index). */
+int sq_log_softmax_at(const float* d_logits, size_t n, uint32_t idx, double* out);
 
 /* ---- measurement -----------------------------------------------------
  * Replays one kernel of the context's decode step `iters` times on the

@@ -201,6 +201,11 @@ int sq_ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms) 
     return ctx_prefill_phases(c, ids, n, ms);
 }
 
+int sq_ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* logp) {
+    if (!c) return set_error(SQ_ERR_ARG, "score: null context");
+    return ctx_score(c, ids, n, burn, logp);
+}
+
 int sq_ctx_act_taps(sq_ctx* c, int enable) {
     if (!c) return set_error(SQ_ERR_ARG, "act_taps: null context");
     return ctx_set_taps(c, enable != 0);
@@ -472,6 +477,21 @@ int sq_elementwise_add(float* d_a, const float* d_b, size_t n) {
 int sq_softmax(const float* d_in, float* d_out, size_t n) {
     if (n == 0) return set_error(SQ_ERR_EMPTY, "softmax: EmptyInput");
     return finish(launch_softmax_row(nullptr, d_in, d_out, (int)n));
+}
+
+int sq_log_softmax_at(const float* d_logits, size_t n, uint32_t idx, double* out) {
+    if (!d_logits || !out) return set_error(SQ_ERR_ARG, "log_softmax_at: null argument");
+    if (n == 0) return set_error(SQ_ERR_EMPTY, "log_softmax_at: EmptyInput");
+    if (idx >= n) return set_error(SQ_ERR_ARG, "log_softmax_at: index out of range");
+    if (n > (size_t)INT32_MAX) return set_error(SQ_ERR_SHAPE, "log_softmax_at: row too long");
+    Tmp id, val;
+    int st;
+    if ((st = id.alloc(4)) || (st = val.alloc(8))) return st;
+    SQ_HIP_CHECK(hipMemcpy(id.p, &idx, 4, hipMemcpyHostToDevice));
+    if ((st = launch_log_softmax_at(nullptr, d_logits, (int)n, (const uint32_t*)id.p, (double*)val.p))) return st;
+    if ((st = finish(0))) return st;
+    SQ_HIP_CHECK(hipMemcpy(out, val.p, 8, hipMemcpyDeviceToHost));
+    return 0;
 }
 
 int sq_greedy(const float* d_logits, size_t n, uint32_t* token) {

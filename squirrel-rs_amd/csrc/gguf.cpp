@@ -214,7 +214,21 @@ int GGUFFile::parse(const uint8_t* data, size_t sz) {
         std::string name = ti.name;
         tensors[name] = std::move(ti);
     }
-    data_offset = (c.pos + kAlign - 1) & ~(kAlign - 1);
+    // The reference always pads to 32 bytes (gguf_file.rs:10,44-46); llama.cpp
+    // writes general.alignment (a power-of-two u32, 32 unless chosen
+    // otherwise) and pads the data section and every tensor to it.  Honouring
+    // the key reads every file the reference reads (alignment 32) and also
+    // files written with another alignment.
+    uint64_t align = kAlign;
+    auto al = meta.find("general.alignment");
+    if (al != meta.end()) {
+        const uint64_t a = al->second.u;
+        if (al->second.type != GT_U32 || a == 0 || (a & (a - 1)) != 0)
+            return set_error(SQ_ERR_FORMAT, "general.alignment must be a power-of-two u32");
+        align = a;
+    }
+    alignment = align;
+    data_offset = (c.pos + align - 1) & ~(align - 1);
     return 0;
 }
 

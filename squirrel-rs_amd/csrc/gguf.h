@@ -65,6 +65,7 @@ class GGUFFile {
     std::unordered_map<std::string, GGUFValue> meta;
     std::unordered_map<std::string, GGUFTensorInfo> tensors;
     uint64_t data_offset = 0;
+    uint64_t alignment = 32;  // general.alignment when present
     const uint8_t* base = nullptr;
     size_t size = 0;
 

@@ -352,6 +352,37 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const float* logits,
     }
 }
 
+// log p(idx) under softmax(logits), in f64 (src/bin/perplexity.rs:112-117):
+// the maximum folded in f32 with NaN entries skipped (f32::max), the sum of
+// exp(f64(l) - max) in f64, then f64(l[idx]) - max - ln(sum).  The sum is a
+// fixed-order tree over the workgroup, not the reference's sequential fold,
+// so the two agree to f64 rounding.
+__global__ __launch_bounds__(1024) void log_softmax_at_kernel(const float* __restrict__ logits, int n,
+                                                              const uint32_t* __restrict__ idx,
+                                                              double* __restrict__ out) {
+    __shared__ float s_m[16];
+    __shared__ double s_s[16];
+    const int tid = threadIdx.x;
+    float m = -INFINITY;
+    for (int i = tid; i < n; i += 1024) m = fmaxf(m, logits[i]);
+    m = sq_wave_max(m);
+    if ((tid & 63) == 0) s_m[tid >> 6] = m;
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int w = 0; w < 16; w++) mx = fmaxf(mx, s_m[w]);
+    const double md = (double)mx;
+    double s = 0.0;
+    for (int i = tid; i < n; i += 1024) s += exp((double)logits[i] - md);
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((tid & 63) == 0) s_s[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) {
+        double tot = 0.0;
+        for (int w = 0; w < 16; w++) tot += s_s[w];
+        *out = (double)logits[*idx] - md - log(tot);
+    }
+}
+
 // Per-block exact integer sums of one quantized activation row against one
 // weight row, in the same lane layout as the decode matvec.
 __global__ __launch_bounds__(64) void block_isums_kernel(const int8_t* aq, MatView w, int row,
@@ -475,6 +506,11 @@ int launch_block_isums(hipStream_t s, const int8_t* aq, const MatView& w, int wt
     v.wtype = wtype;
     hipLaunchKernelGGL(block_isums_kernel, dim3(1), dim3(64), 0, s, aq, v, row, out);
     return check_launch("block_isums");
+}
+
+int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint32_t* idx, double* out) {
+    hipLaunchKernelGGL(log_softmax_at_kernel, dim3(1), dim3(1024), 0, s, logits, n, idx, out);
+    return check_launch("log_softmax_at");
 }
 
 int launch_copy_i32(hipStream_t s, const int* src, int* dst) {

@@ -116,6 +116,8 @@ int launch_argmax_partials(hipStream_t s, const float* logits, int n, float* par
 int launch_block_isums(hipStream_t s, const int8_t* aq, const MatView& w, int wtype, int row,
                        int32_t* out);
 int launch_copy_i32(hipStream_t s, const int* src, int* dst);
+// out = log p(*idx) under softmax(logits[0..n)) in f64 (*idx < n).
+int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint32_t* idx, double* out);
 
 // ---- prefill matmul (k_gemm.hip) ----------------------------------------
 // out[m, rows] (+)= in[m, k] @ W.  a8: activations given as Q8_0 (aq/ad,

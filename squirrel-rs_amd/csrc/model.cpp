@@ -820,7 +820,8 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
         (st = dmalloc(&c->pv, c->n_parts)) ||
         (st = dmalloc(&c->pi, c->n_parts)) || (st = dmalloc(&c->pn, c->n_parts)) ||
         (st = dmalloc(&c->dbg_normed, D)) || (st = dmalloc(&c->last_hidden, D)) || (st = dmalloc(&c->head_qs, D)) ||
-        (st = dmalloc(&c->head_d, D / 32)))
+        (st = dmalloc(&c->head_d, D / 32)) || (st = dmalloc(&c->d_sids, max_pos + 1)) ||
+        (st = dmalloc(&c->d_logp, max_pos + 1)))
         return fail(st);
     he = hipHostMalloc((void**)&c->h_pinned, (max_pos + 16) * sizeof(uint32_t), hipHostMallocDefault);
     if (he != hipSuccess) return fail(set_error(SQ_ERR_HIP, std::string("hipHostMalloc: ") + hipGetErrorString(he)));
@@ -878,6 +879,7 @@ void ctx_destroy(sq_ctx* c) {
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
     dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad); dfree(c->p_split);
     dfree(c->d_layers); dfree(c->s_stream); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
+    dfree(c->d_sids); dfree(c->d_logp);
     if (c->h_pinned) (void)hipHostFree(c->h_pinned);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
@@ -908,11 +910,52 @@ int ctx_forward(sq_ctx* c, const uint32_t* ids, size_t n) {
     return 0;
 }
 
+int ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* logp) {
+    if (!c || !ids || !logp) return set_error(SQ_ERR_ARG, "score: null argument");
+    if (burn == 0 || burn >= n) return set_error(SQ_ERR_ARG, "score: the burn-in must leave 1 to n - 1 scored tokens");
+    if (n - 1 > c->max_pos)
+        return set_error(SQ_ERR_CACHE_FULL, "score: a window of " + std::to_string(n) + " tokens needs " +
+                                                std::to_string(n - 1) + " positions; the context holds " +
+                                                std::to_string(c->max_pos));
+    const int V = c->m->cfg.vocab;
+    for (size_t i = 0; i < n; i++)
+        if ((int64_t)ids[i] >= V) return set_error(SQ_ERR_ARG, "score: token id out of range");
+    // A fresh cache per window (perplexity.rs:69-70).  The token history
+    // restarts with the position: every head step appends to it, and it
+    // holds max_pos + 1 entries.
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    c->seq_len = 0;
+    SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
+    SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
+    int st = ctx_forward(c, ids, burn);
+    if (st) return st;
+    // ctx_forward synchronized before staging the burn-in ids; the window
+    // goes to the device behind the prefill on the same stream.
+    SQ_HIP_CHECK(hipMemcpyAsync(c->d_sids, ids, n * 4, hipMemcpyHostToDevice, c->stream));
+    // Every step stays on the device: the scored token's log-probability is
+    // taken from the logits in place, and the same id is fed to the next
+    // decode step from device memory.
+    for (size_t i = burn; i < n; i++) {
+        if ((st = launch_log_softmax_at(c->stream, c->logits, V, c->d_sids + i, c->d_logp + (i - burn)))) return st;
+        if (i + 1 < n) {
+            if ((st = launch_copy_i32(c->stream, (const int*)(c->d_sids + i), (int*)c->d_token))) return st;
+            if ((st = run_decode_step(c))) return st;
+            c->seq_len++;
+        }
+    }
+    SQ_HIP_CHECK(hipMemcpyAsync(logp, c->d_logp, (n - burn) * sizeof(double), hipMemcpyDeviceToHost, c->stream));
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    c->last_rows = 1;
+    c->last_tapped = false;
+    return ctx_check(c);
+}
+
 int ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms) {
     if (n < 2) return set_error(SQ_ERR_ARG, "prefill_phases: needs a prompt of at least 2 tokens");
     SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
     c->seq_len = 0;
     SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
+    SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
     c->prof = true;
     int st = ctx_forward(c, ids, n);
     c->prof = false;

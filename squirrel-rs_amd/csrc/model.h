@@ -130,6 +130,8 @@ struct sq_ctx {
     int* s_error = nullptr;
     unsigned long long* s_trace = nullptr;  // step timeline when enabled
 
+    uint32_t* d_sids = nullptr;    // the window being scored [max_pos + 1]
+    double* d_logp = nullptr;      // its log-probabilities [max_pos + 1]
     uint32_t* h_pinned = nullptr;  // pinned staging for ids / tokens
     hipGraphExec_t graph = nullptr;
     hipGraph_t graph_def = nullptr;
@@ -169,6 +171,10 @@ int ctx_generate(sq_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t max_
                  uint32_t* out, size_t* n_out, double* step_ms);
 int ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_t* bytes);
 int ctx_set_taps(sq_ctx* c, bool on);
+// Teacher-forced scoring of one window on a reset context (perplexity.rs:61-110):
+// prefill ids[0, burn), then for i in [burn, n): logp[i - burn] = log p(ids[i])
+// and, while i + 1 < n, one decode step on ids[i].
+int ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* logp);
 // Runs a prefill of ids on a reset context with HIP events between launch
 // groups; ms[0..3] = int8 matmuls, attention, everything else, whole prefill.
 int ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms);

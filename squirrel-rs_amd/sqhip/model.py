@@ -187,6 +187,16 @@ class ModelContext:
         self._last_rows = ids.size
         return {"matmul": float(ms[0]), "attention": float(ms[1]), "other": float(ms[2]), "total": float(ms[3])}
 
+    def score(self, window_ids, burn: int) -> np.ndarray:
+        """One perplexity window (sq_ctx_score, perplexity.rs:61-110): resets
+        the cache, prefills window[:burn], then teacher-forces the rest and
+        returns log p(window[i]) for i in [burn, len) as float64."""
+        ids = np.ascontiguousarray(window_ids, dtype=np.uint32)
+        out = np.zeros(max(0, ids.size - burn), np.float64)
+        check(lib().sq_ctx_score(self.h, ids.ctypes.data, ids.size, burn, out.ctypes.data))
+        self._last_rows = 1
+        return out
+
     def close(self) -> None:
         if self.h:
             lib().sq_ctx_free(self.h)

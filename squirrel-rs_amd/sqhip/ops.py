@@ -173,6 +173,13 @@ def softmax(a: DeviceArray, out: DeviceArray) -> None:
     check(lib().sq_softmax(a.ptr, out.ptr, a.size))
 
 
+def log_softmax_at(logits: DeviceArray, idx: int) -> float:
+    """log p(idx) under softmax(logits) in f64 (perplexity.rs:112-117)."""
+    v = C.c_double()
+    check(lib().sq_log_softmax_at(logits.ptr, logits.size, idx, C.byref(v)))
+    return v.value
+
+
 def greedy(logits: DeviceArray) -> int:
     """GreedySampler::sample (src/samplers/greedy.rs:6-15) on the device."""
     t = C.c_uint32()

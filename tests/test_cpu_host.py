@@ -234,6 +234,65 @@ def test_load_path_errors(tmp_path, case, code):
             O.LlamaConfig(GGUFFile(p))
 
 
+# ----------------------------------------------------------- llama.cpp layout
+
+LLAMACPP_VARIANTS = {
+    # alignment, write the key, llama.vocab_size, rope scaling keys, rope.dimension_count
+    "align32": dict(alignment=32),
+    "align64": dict(alignment=64),
+    "align256": dict(alignment=256),
+    "no_alignment_key": dict(alignment=32, alignment_key=False),
+    "vocab_size_key": dict(alignment=32, vocab_size_key=True),
+    "rope_scaling_keys": dict(alignment=32, rope_scaling_keys=True),
+    "no_head_dim_key": dict(alignment=32, head_dim_key=False),
+}
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+@pytest.mark.parametrize("variant", sorted(LLAMACPP_VARIANTS))
+def test_llamacpp_layout_inspects(tmp_path, wtype, variant):
+    """Files in llama.cpp's layout (its metadata set, token and merge arrays,
+    rope_freqs.weight, general.alignment padding) read to the same config as
+    the synthetic model they were rewritten from (config.rs:29-73): the
+    vocabulary comes from tokenizer.ggml.tokens when llama.vocab_size is
+    absent, head_dim from dim / heads when rope.dimension_count is absent, and
+    the llama3 RoPE table from the defaults or equal keys."""
+    from llamacpp_gguf import rewrite_llamacpp
+    src = str(tmp_path / "src.gguf")
+    sqhip.write_synthetic_gguf(src, wtype, seed=3, **SMALL)
+    dst = str(tmp_path / "llamacpp.gguf")
+    rewrite_llamacpp(src, dst, **LLAMACPP_VARIANTS[variant])
+    code0, want, inv0 = inspect(src)
+    code, got, inv = inspect(dst)
+    assert code0 == 0 and code == 0, lib().sq_last_error()
+    for f in ("n_layers", "dim", "ffn_dim", "n_heads", "n_kv_heads", "head_dim", "vocab", "context_length",
+              "bos", "eos", "wtype", "tied_output", "rope_base", "rms_eps", "weight_bytes"):
+        assert getattr(got, f) == getattr(want, f), f
+    assert np.array_equal(inv, inv0)
+    # the fixture itself: every tensor at data_start + offset, aligned as declared
+    if variant != "no_alignment_key":
+        a = LLAMACPP_VARIANTS[variant]["alignment"]
+        raw = np.fromfile(dst, np.uint8)
+        g = GGUFFile(src)
+        if a == 32:  # the fixed-32 reader restating the reference finds the same bytes
+            d = GGUFFile(dst)
+            for n in g.tensors:
+                assert np.array_equal(d.tensor_bytes(n), g.tensor_bytes(n)), n
+        assert len(raw) % a == 0
+
+
+@pytest.mark.parametrize("bad", [("u32", 48), ("u32", 0), ("f32", 32.0)])
+def test_llamacpp_bad_alignment_is_a_format_error(tmp_path, bad):
+    """general.alignment must be a power-of-two u32 (as llama.cpp requires)."""
+    w = full_model(base_meta(Writer()))
+    if bad[0] == "u32":
+        w.u32("general.alignment", bad[1])
+    else:
+        w.f32("general.alignment", bad[1])
+    code, _, _ = inspect(write(tmp_path, w.bytes()))
+    assert code == 17 and "alignment" in lib().sq_last_error().decode()
+
+
 # ----------------------------------------------------------- argument checks
 
 def test_operator_shape_errors_without_device():

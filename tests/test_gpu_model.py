@@ -351,6 +351,117 @@ def test_no_kv_cache_mode(tiny_gguf):
         seq.append(gen[step])
 
 
+def seq_log_softmax_at(logits, idx):
+    """log p(idx) as perplexity.rs:112-117 writes it: f32 max fold, a
+    sequential f64 sum of exp(l - max), then the log."""
+    mx = np.float64(np.nanmax(logits))
+    return float(np.float64(logits[idx]) - mx - np.log(np.cumsum(np.exp(logits.astype(np.float64) - mx))[-1]))
+
+
+@pytest.fixture(scope="module")
+def ppl_gguf(model_dir):
+    """A tiny model whose BOS / EOS ids lie inside its vocabulary."""
+    from conftest import TINY_G2
+    path = str(model_dir / "ppl_q8_0.gguf")
+    sq.write_synthetic_gguf(path, "Q8_0", seed=21, bos=1, eos=2, **TINY_G2)
+    return path
+
+
+@pytest.mark.parametrize("decode", ["persistent", "multi_kernel"])
+def test_score_window_matches_teacher_forced_forward(ppl_gguf, decode):
+    """sq_ctx_score (one perplexity window, perplexity.rs:61-110): its
+    log-probabilities equal the reference's f64 log-softmax of the logits a
+    teacher-forced forward loop produces (1e-12), and those logits are
+    checked against the oracle phase-locked."""
+    m = sq.Llama3_2(ppl_gguf)
+    r = np.random.default_rng(4)
+    window = np.concatenate([[1], r.integers(3, m.vocab, 23)]).astype(np.uint32)
+    burn = 12
+    c = m.new_context(32, persistent=decode == "persistent")
+    got = c.score(window, burn)
+    assert got.shape == (window.size - burn,)
+    seq = [window[:burn]] + [int(t) for t in window[burn:-1]]
+    logits, _, (_, _, blocks) = run_gpu(ppl_gguf, seq, max_pos=32, persistent=decode == "persistent")
+    check_logits(ppl_gguf, seq, logits, blocks, f"score/{decode}", max_pos=32)
+    want = np.array([seq_log_softmax_at(l, int(window[burn + i])) for i, l in enumerate(logits)])
+    err = float(np.abs(got - want).max())
+    print(f"score vs forward loop: max |d logp| {err:.2e}")
+    assert err < 1e-12
+    # the context is reusable: a second window scores the same way
+    assert np.array_equal(c.score(window, burn), got)
+
+
+def test_perplexity_harness(ppl_gguf):
+    """sqhip.perplexity over a token stream: windows of BOS + n_ctx - 1
+    tokens, burn-in n_ctx / 2, NLL accumulated in the reference's order;
+    equal (1e-12) to the same computation on teacher-forced forward logits."""
+    from sqhip.perplexity import perplexity
+    m = sq.Llama3_2(ppl_gguf)
+    r = np.random.default_rng(9)
+    ids = r.integers(3, m.vocab, 3 * 15 + 7).astype(np.uint32)
+    res = perplexity(m, ids, n_ctx=16)
+    assert res["windows"] == 3 and res["scored_tokens"] == 3 * 8 and res["burn"] == 8
+    total, scored = 0.0, 0
+    for w in range(3):
+        window = np.concatenate([[1], ids[w * 15:(w + 1) * 15]]).astype(np.uint32)
+        seq = [window[:8]] + [int(t) for t in window[8:-1]]
+        logits, _, _ = run_gpu(ppl_gguf, seq, max_pos=16, taps=False)
+        wnll = 0.0
+        for i, l in enumerate(logits):
+            wnll -= seq_log_softmax_at(l, int(window[8 + i]))
+        total += wnll
+        scored += len(logits)
+    want = total / scored
+    print(f"perplexity nll/token {res['nll_per_token']:.9f} (forward loop {want:.9f}), ppl {res['ppl']:.4f}")
+    assert abs(res["nll_per_token"] - want) < 1e-12 and scored == res["scored_tokens"]
+
+
+def test_text_generation_streams_the_greedy_sequence(model_dir, monkeypatch):
+    """The text front end (text_generator.rs:38-101 with a tokenizer.json):
+    the tokens it streams are the id-level generator's greedy sequence for
+    the encoded prompt (that sequence is checked against the oracle in
+    test_generate_matches_forward_loop), and the printed deltas add up to
+    the decoded text."""
+    pytest.importorskip("tokenizers")
+    import io
+    from conftest import TINY_G2
+    from sqhip.text import Tokenizer, generate_text
+    from tokenizer_fixture import write_tokenizer
+    tpath = str(model_dir / "tokenizer.json")
+    bos, eos = write_tokenizer(tpath)
+    mpath = str(model_dir / "text_q8_0.gguf")
+    sq.write_synthetic_gguf(mpath, "Q8_0", seed=5, bos=bos, eos=eos, **TINY_G2)
+    m, tok = sq.Llama3_2(mpath), Tokenizer(tpath)
+    monkeypatch.setenv("SQUIRREL_IGNORE_EOS", "1")
+    prompt = "The capital of France is"
+    out, log = io.StringIO(), io.StringIO()
+    text = generate_text(m, tok, prompt, 10, out=out, log=log)
+    ids = tok.encode(prompt, True)
+    want, _ = sq.TextTokenGenerator(m, m.new_context(64)).generate(ids, 10, ignore_eos=True)
+    assert text == tok.decode(want) and out.getvalue() == text + "\n"
+    assert log.getvalue().splitlines()[0] == f"[prompt: {len(ids)} tokens]"
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+def test_llamacpp_layout_files(tiny_gguf, model_dir, wtype):
+    """Files laid out as llama.cpp writes them (its metadata, token arrays,
+    rope_freqs.weight, data padded to general.alignment 32 / 64 / 256) load
+    and run bit-identically to the synthetic model they were rewritten from;
+    that model is checked against the oracle phase-locked (model.rs:45-97)."""
+    from llamacpp_gguf import rewrite_llamacpp
+    src = tiny_gguf(wtype, "g2")
+    cfg = O.OracleModel(src).cfg
+    seq = teacher_seq(cfg.vocab, n_prompt=9, n_decode=3, seed=11)
+    want, _, (_, _, blocks) = run_gpu(src, seq)
+    check_logits(src, seq, want, blocks, f"{wtype}/source")
+    for a in (32, 64, 256):
+        dst = str(model_dir / f"llamacpp_{wtype}_{a}.gguf")
+        rewrite_llamacpp(src, dst, alignment=a)
+        got, _, _ = run_gpu(dst, seq, taps=False)
+        for step, (g, w) in enumerate(zip(got, want)):
+            assert np.array_equal(g, w), f"alignment {a}, step {step}"
+
+
 def test_a32_paths_refuse_loudly(tiny_gguf):
     """The switched-off paths fail with an error instead of running."""
     with pytest.raises(sq.LLMError) as e:

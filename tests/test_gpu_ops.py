@@ -321,6 +321,32 @@ def test_greedy_matches_oracle(case):
     assert ops.greedy(DeviceArray.from_numpy(x)) == O.greedy(x)
 
 
+def test_log_softmax_at_closed_forms():
+    """log p(idx) of the perplexity harness (perplexity.rs:112-117) on inputs
+    whose value is known in closed form, and on a vocabulary-sized row
+    against scipy's log-softmax (an independent formulation), in f64."""
+    from scipy.special import log_softmax
+    ls = lambda x, i: ops.log_softmax_at(DeviceArray.from_numpy(np.asarray(x, np.float32)), i)  # noqa: E731
+    assert abs(ls(np.full(1000, 3.7), 17) - (-np.log(1000.0))) < 1e-12
+    x = np.array([0.0, -np.inf, -np.inf, np.log(3.0)], np.float32)
+    assert abs(ls(x, 0) - np.log(1.0 / (1.0 + float(np.exp(np.float64(np.float32(np.log(3.0)))))))) < 1e-12
+    assert ls(x, 1) == -np.inf
+    assert abs(ls([1e30, 1e30], 1) - np.log(0.5)) < 1e-15
+    assert np.isnan(ls([1.0, np.nan, 2.0], 0))            # exp(NaN - max) poisons the sum
+    a, b, k, n = 2.5, -1.25, 37, 4096
+    x = np.full(n, b, np.float32)
+    x[:k] = a
+    want = (a - a) - np.log(k + (n - k) * np.exp(b - a))
+    assert abs(ls(x, 3) - want) < 1e-12
+    r = rng(5)
+    x = (r.standard_normal(128256) * 3).astype(np.float32)
+    ref = log_softmax(x.astype(np.float64))
+    for i in (0, 1, 77777, 128255, int(np.argmax(x))):
+        assert abs(ls(x, i) - ref[i]) < 1e-11
+    with pytest.raises(sq.SqError):
+        ls(x, 128256)
+
+
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
 def test_embed_bit_exact(wtype):
     if wtype == O.BF16:
