@@ -374,6 +374,200 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
             }
 }
 
+// ---- 128 x 128 tiles on the 32 x 32 matrix instructions ----------------------
+// The same contraction with four times the output per workgroup, for inputs
+// of at least 128 rows.  v_mfma_i32_32x32x32_i8 (the full int8 rate of
+// gfx950; the 16 x 16 x 32 form runs at half of it) gives the exact i32 isum
+// of a 32 x 32 tile for one block: lane l supplies 16 bytes of row l % 32,
+// half l / 32 of the block, and the other operand alike.  The scale products
+// come from one v_mfma_f32_32x32x8_f16 per tile and block (lanes 0-31 hold
+// the row's block scales in k-slots 0-1, the others zeros; the column operand
+// of block b holds sw_b in slot b).  Result element r of lane l is row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  Each of the four wavefronts
+// computes 64 x 64 (2 x 2 tiles).  K advances two blocks per chunk through
+// two LDS buffers with one barrier per chunk; every thread keeps two chunks'
+// global loads in registers, issued two chunks ahead of their use.
+constexpr int M8_T = 128;
+constexpr int M8_KB = 2;           // blocks per chunk
+constexpr int M8_KC = M8_KB * 32;  // bytes per row per chunk
+constexpr int M8_LD = M8_KC + 16;  // LDS row stride: 16-byte reads of 8 consecutive rows cover all banks
+
+typedef int m8_v16i __attribute__((ext_vector_type(16)));
+typedef float m8_v16f __attribute__((ext_vector_type(16)));
+
+struct M8Loads {
+    sq_v4i a[2];  // activation pieces (row p / 4, 16-byte unit p % 4 for p = tid, tid + 256)
+    sq_v4i w[2];  // Q8_0: weight pieces as a[]; Q4_0: w[0] is one packed block
+    uint16_t sa, sw;
+    bool va, vw;  // the scales are in range (applied when staged)
+};
+
+template <int WT>
+__global__ __launch_bounds__(256, 2) void gemm_mfma128_kernel(MatView w, const int8_t* __restrict__ aq,
+                                                              const uint16_t* __restrict__ ad, int m_rows,
+                                                              float* __restrict__ out, int ldo, int accumulate,
+                                                              int kbs, size_t split_stride) {
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][M8_T * M8_LD];
+    __shared__ __attribute__((aligned(16))) int8_t sW[2][M8_T * M8_LD];
+    // sSa[buf][row][slot]: the chunk's two block scales in slots 0-1; slots
+    // 2-3 and row M8_T stay zero.  sSw[buf][b][col]: sw_b in slot b.
+    __shared__ __attribute__((aligned(16))) uint16_t sSa[2][M8_T + 1][4];
+    __shared__ __attribute__((aligned(16))) uint16_t sSw[2][M8_KB][M8_T][4];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int K = w.k, KB = K >> 5;
+    const int m0 = blockIdx.y * M8_T, n0 = blockIdx.x * M8_T;
+    const int kb_begin = blockIdx.z * kbs, kb_end = min(KB, kb_begin + kbs);
+    out += blockIdx.z * split_stride;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int fr = lane & 31, fh = lane >> 5;
+
+    // Clear what staging never writes (slots 2-3, row M8_T), so no clear can
+    // land on a scale another thread has already staged; the first chunk's
+    // barrier publishes both.
+    for (int i = tid; i < 2 * (M8_T + 1); i += 256) {
+        uint32_t* z = (uint32_t*)&sSa[i / (M8_T + 1)][i % (M8_T + 1)][0];
+        z[1] = 0;
+        if (i % (M8_T + 1) == M8_T) z[0] = 0;
+    }
+
+    // Every thread issues the same loads for every chunk, without branches:
+    // rows and blocks past the end read the last valid row and block, and
+    // their scales are set to zero, so their terms are fma(isum, 0, acc) =
+    // acc and rows past the end are never stored.  With a fixed count of
+    // loads per chunk the wait before staging one register set can leave the
+    // other set's loads in flight.
+    auto fetch = [&](M8Loads& L, int kb0) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int p = tid + 256 * q, r = p >> 2, u = p & 3;
+            const int kb = min(kb0 + (u >> 1), KB - 1);
+            const size_t ra = (size_t)min(m0 + r, m_rows - 1), rw = (size_t)min(n0 + r, w.rows - 1);
+            L.a[q] = *(const sq_v4i*)(aq + ra * K + kb * 32 + 16 * (u & 1));
+            if constexpr (WT == WT_Q8_0) L.w[q] = *(const sq_v4i*)((const int8_t*)w.qs + rw * K + kb * 32 + 16 * (u & 1));
+        }
+        if constexpr (WT == WT_Q4_0) {
+            const int r = tid >> 1, kb = min(kb0 + (tid & 1), KB - 1);
+            L.w[0] = *(const sq_v4i*)((const uint8_t*)w.qs + (size_t)min(n0 + r, w.rows - 1) * (K / 2) + kb * 16);
+        }
+        const int r = tid & 127, kb = kb0 + (tid >> 7), kbc = min(kb, KB - 1);
+        const uint16_t sa = ad[(size_t)min(m0 + r, m_rows - 1) * KB + kbc];
+        const uint16_t sw = w.scale[(size_t)min(n0 + r, w.rows - 1) * KB + kbc];
+        L.sa = sa;
+        L.sw = sw;
+        L.va = m0 + r < m_rows && kb < kb_end;
+        L.vw = n0 + r < w.rows && kb < kb_end;
+    };
+    auto stage = [&](const M8Loads& L, int buf) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int p = tid + 256 * q, r = p >> 2, u = p & 3;
+            *(sq_v4i*)(sA[buf] + r * M8_LD + 16 * u) = L.a[q];
+            if constexpr (WT == WT_Q8_0) *(sq_v4i*)(sW[buf] + r * M8_LD + 16 * u) = L.w[q];
+        }
+        if constexpr (WT == WT_Q4_0) {
+            // byte j holds element j (low nibble) and j + 16 (high nibble);
+            // per byte, nibble - 8 as a signed byte (see gemm_mfma_kernel)
+            const int r = tid >> 1, b = tid & 1;
+            const unsigned wd[4] = {(unsigned)L.w[0].x, (unsigned)L.w[0].y, (unsigned)L.w[0].z, (unsigned)L.w[0].w};
+            int lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = (int)((((wd[i] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+                hi[i] = (int)(((((wd[i] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+            }
+            *(sq_v4i*)(sW[buf] + r * M8_LD + 32 * b) = sq_v4i{lo[0], lo[1], lo[2], lo[3]};
+            *(sq_v4i*)(sW[buf] + r * M8_LD + 32 * b + 16) = sq_v4i{hi[0], hi[1], hi[2], hi[3]};
+        }
+        const int r = tid & 127, b = tid >> 7;
+        sSa[buf][r][b] = L.va ? L.sa : (uint16_t)0;
+        *(uint2*)&sSw[buf][b][r][0] = make_uint2(L.vw ? (unsigned)L.sw << (16 * b) : 0u, 0u);
+    };
+
+    m8_v16f acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+
+    auto compute = [&](int buf) {
+        const int8_t* A = sA[buf];
+        const int8_t* W = sW[buf];
+        mq_v4h sa[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) sa[i] = *(const mq_v4h*)&sSa[buf][fh == 0 ? wm + 32 * i + fr : M8_T][0];
+        // one block's operands at a time: the row and column fragments and
+        // the column scale operands of the 2 x 2 tiles
+        sq_v4i af[2], bf[2];
+        mq_v4h sw[2];
+        auto operands = [&](int b) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                af[i] = *(const sq_v4i*)(A + (wm + 32 * i + fr) * M8_LD + 32 * b + 16 * fh);
+                bf[i] = *(const sq_v4i*)(W + (wn + 32 * i + fr) * M8_LD + 32 * b + 16 * fh);
+                sw[i] = *(const mq_v4h*)&sSw[buf][b][wn + 32 * i + fr][0];
+            }
+        };
+        // Products for (block, tile) pairs k = 4 b + t, issued one pair ahead
+        // of the pair being folded in.
+        const m8_v16i izero = {};
+        const m8_v16f fzero = {};
+        m8_v16i d[2];
+        m8_v16f sc[2];
+        operands(0);
+        d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0], bf[0], izero, 0, 0, 0);
+        sc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[0], sw[0], fzero, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4 * M8_KB; k++) {
+            if (k + 1 < 4 * M8_KB) {
+                const int i = ((k + 1) >> 1) & 1, j = (k + 1) & 1;
+                if (((k + 1) & 3) == 0) operands((k + 1) >> 2);
+                d[(k + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], izero, 0, 0, 0);
+                sc[(k + 1) & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[i], sw[j], fzero, 0, 0, 0);
+            }
+            const int t = k & 3;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                // the combine of the reference's aarch64 kernels (dot_prod.rs:189-252):
+                // acc = fma(f32(isum), sa * sw, acc)
+                acc[t][r] = fmaf((float)d[k & 1][r], sc[k & 1][r], acc[t][r]);
+            }
+        }
+    };
+
+    // Chunk c's loads are in set c % 2 and its tiles in buffer c % 2.  Once a
+    // set is staged it takes chunk c + 2; buffer c % 2 was last read in chunk
+    // c - 2, before the previous chunk's barrier.
+    // The loop body is straight-line code over two chunks (an odd count gets
+    // one chunk past kb_end, whose zero scales fold nothing), so the wait
+    // before staging a set leaves the other set's loads in flight.
+    M8Loads L0, L1;
+    const int n_chunks = (kb_end - kb_begin + M8_KB - 1) / M8_KB;
+    fetch(L0, kb_begin);
+    fetch(L1, kb_begin + M8_KB);
+    for (int c = 0; c < n_chunks; c += 2) {
+        stage(L0, 0);
+        __syncthreads();
+        fetch(L0, kb_begin + (c + 2) * M8_KB);
+        compute(0);
+        stage(L1, 1);
+        __syncthreads();
+        fetch(L1, kb_begin + (c + 3) * M8_KB);
+        compute(1);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + wm + 32 * (t >> 1) + 8 * (r >> 2) + 4 * fh + (r & 3);
+            const int n = n0 + wn + 32 * (t & 1) + fr;
+            if (m < m_rows && n < w.rows) {
+                float* o = out + (size_t)m * ldo + n;
+                *o = accumulate ? *o + acc[t][r] : acc[t][r];
+            }
+        }
+}
+
 // out[r, c] (+)= the sum of the K-split partial tiles, in split order.
 __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ ws, int splits, size_t stride,
                                                         int m, int n, float* __restrict__ out, int ldo,
@@ -420,6 +614,63 @@ int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
     return 0;
 }
 
+// 128 x 128 tiles.  They pay where the output alone gives at least 512 of
+// them (two workgroups on each CU, for example the gate/up projection of a
+// 2048-token prompt: 2048 tiles, 230 us against 265 us on 64 x 64 tiles);
+// smaller grids return 1 (nothing launched) and take the 64 x 64 kernel,
+// which holds four workgroups per CU (256 tiles of 128 x 128: 122 against
+// 92 us).  When pinned to this tiling, a grid of fewer than 512 workgroups
+// splits K while the workspace holds the partial tiles.
+template <int WT>
+int run_mfma128(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
+                bool acc, float* ws, size_t ws_floats, bool force) {
+    const int gx = (w.rows + M8_T - 1) / M8_T, gy = (m + M8_T - 1) / M8_T;
+    const int KB = w.k / 32, chunks = (KB + M8_KB - 1) / M8_KB;
+    int splits = 1;
+    if (ws != nullptr && gx * gy < 512) {
+        splits = min(chunks, (512 + gx * gy - 1) / (gx * gy));
+        while (splits > 1 && (size_t)splits * m * w.rows > ws_floats) splits--;
+    }
+    if (!force && gx * gy < 512) return 1;
+    const int kbs = ((chunks + splits - 1) / splits) * M8_KB;
+    splits = (KB + kbs - 1) / kbs;
+    hipError_t e;
+    if (splits == 1) {
+        hipLaunchKernelGGL(gemm_mfma128_kernel<WT>, dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0,
+                           KB, (size_t)0);
+    } else {
+        const size_t stride = (size_t)m * w.rows;
+        hipLaunchKernelGGL(gemm_mfma128_kernel<WT>, dim3(gx, gy, splits), dim3(256), 0, s, w, aq, ad, m, ws, w.rows,
+                           0, kbs, stride);
+        e = hipGetLastError();
+        if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+        hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
+                           m, w.rows, out, ldo, acc ? 1 : 0);
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+    return 0;
+}
+
+// SQUIRREL_GEMM_TILE=64 or 128 pins the prefill matmul's tile (a test and
+// measurement aid); unset, inputs of at least 128 rows take the 128 x 128
+// kernel when its grid fills the device.
+int gemm_tile_override() {
+    const char* e = getenv("SQUIRREL_GEMM_TILE");
+    return e ? atoi(e) : 0;
+}
+
+template <int WT>
+int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
+                bool acc, float* ws, size_t ws_floats) {
+    const int tile = gemm_tile_override();
+    if (tile != 64 && (m >= M8_T || tile == 128)) {
+        const int st = run_mfma128<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == 128);
+        if (st != 1) return st;
+    }
+    return run_mfma<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats);
+}
+
 template <int WT, bool A8, int NBL, int MT>
 int run(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, const float* x, int m,
         float* out, int ldo, bool acc) {
@@ -458,11 +709,11 @@ int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_
         // (without a workspace for a K split, inputs below one 64-row tile
         // stay on the VALU kernel, which spreads the weights over more workgroups)
         case WT_Q8_0:
-            if (a8 && (m >= MQ_T || ws != nullptr)) return run_mfma<WT_Q8_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
+            if (a8 && (m >= MQ_T || ws != nullptr)) return run_integer<WT_Q8_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
             return a8 ? dispatch<WT_Q8_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q8_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_Q4_0:
-            if (a8 && (m >= MQ_T || ws != nullptr)) return run_mfma<WT_Q4_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
+            if (a8 && (m >= MQ_T || ws != nullptr)) return run_integer<WT_Q4_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
             return a8 ? dispatch<WT_Q4_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q4_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_BF16:

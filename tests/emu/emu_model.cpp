@@ -85,8 +85,13 @@ int main(int argc, char** argv) {
         sq_memcpy_d2h(got.data(), dy, got.size() * 4);
         or_linear(x.data(), m, k, wt, w.data(), n, want.data(), md);
         double worst = 0;
-        for (size_t i = 0; i < got.size(); i++)
-            worst = std::fmax(worst, std::fabs((double)got[i] - want[i]) / (std::fabs((double)want[i]) + 1e-3));
+        int shown = 0;
+        for (size_t i = 0; i < got.size(); i++) {
+            const double rel = std::fabs((double)got[i] - want[i]) / (std::fabs((double)want[i]) + 1e-3);
+            worst = std::fmax(worst, rel);
+            if (rel > 1e-2 && shown++ < 8)
+                printf("bad row %zu col %zu got %.6g want %.6g\n", i / n, i % n, got[i], want[i]);
+        }
         printf("linear wtype %d m %d k %d n %d mode %d worst_rel %.3e got0 %.6g want0 %.6g\n", wt, m, k, n, md, worst,
                got[0], want[0]);
         return 0;

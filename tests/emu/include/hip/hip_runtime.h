@@ -245,6 +245,56 @@ inline sqemu_v4f mfma_f32_16x16x16f16(sqemu_v4h a, sqemu_v4h b, sqemu_v4f c) {
     }
     return d;
 }
+// 32 x 32 results: element r of lane l is D[8(r/4) + 4(l/32) + r%4][l%32].
+typedef int sqemu_v16i __attribute__((ext_vector_type(16)));
+typedef float sqemu_v16f __attribute__((ext_vector_type(16)));
+inline int mfma32_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+// v_mfma_i32_32x32x32_i8: lane l supplies A[l%32][16(l/32) .. +15] and
+// B[16(l/32) .. +15][l%32].
+inline sqemu_v16i mfma_i32_32x32x32_i8(sqemu_v4i a, sqemu_v4i b, sqemu_v16i c) {
+    uint64_t mine[4];
+    memcpy(&mine[0], &a, 16);
+    memcpy(&mine[2], &b, 16);
+    const uint64_t* all = wave_exchange_n(mine, 4, 0x4003);
+    const int lane = g_lane;
+    const int col = lane & 31;
+    sqemu_v16i d = c;
+    for (int r = 0; r < 16; r++) {
+        const int row = mfma32_row(lane, r);
+        int s = 0;
+        for (int k = 0; k < 32; k++) {
+            const int8_t* pa = (const int8_t*)&all[4 * (row + 32 * (k >> 4))];
+            const int8_t* pb = (const int8_t*)&all[4 * (col + 32 * (k >> 4)) + 2];
+            s += (int)pa[k & 15] * (int)pb[k & 15];
+        }
+        d[r] += s;
+    }
+    return d;
+}
+// v_mfma_f32_32x32x8_f16: lane l supplies A[l%32][4(l/32) .. +3] and
+// B[4(l/32) .. +3][l%32]; the sum is formed in double and rounded once (exact
+// in the kernels' use).
+inline sqemu_v16f mfma_f32_32x32x8f16(sqemu_v4h a, sqemu_v4h b, sqemu_v16f c) {
+    uint64_t mine[2];
+    memcpy(&mine[0], &a, 8);
+    memcpy(&mine[1], &b, 8);
+    const uint64_t* all = wave_exchange_n(mine, 2, 0x4004);
+    const int lane = g_lane;
+    const int col = lane & 31;
+    sqemu_v16f d = c;
+    for (int r = 0; r < 16; r++) {
+        const int row = mfma32_row(lane, r);
+        double s = d[r];
+        for (int k = 0; k < 8; k++) {
+            _Float16 av, bv;
+            memcpy(&av, (const char*)&all[2 * (row + 32 * (k >> 2))] + 2 * (k & 3), 2);
+            memcpy(&bv, (const char*)&all[2 * (col + 32 * (k >> 2)) + 1] + 2 * (k & 3), 2);
+            s += (double)av * (double)bv;
+        }
+        d[r] = (float)s;
+    }
+    return d;
+}
 // v_mfma_f32_16x16x8_bf16-style operands are not emulated.
 }  // namespace sqemu
 
@@ -261,6 +311,8 @@ inline sqemu_v4f mfma_f32_16x16x16f16(sqemu_v4h a, sqemu_v4h b, sqemu_v4f c) {
 #define __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, x, y, z) ::sqemu::mfma_i32_16x16x32_i8((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) ::sqemu::mfma_f32_16x16x4f32((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, x, y, z) ::sqemu::mfma_f32_16x16x16f16((a), (b), (c))
+#define __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, x, y, z) ::sqemu::mfma_i32_32x32x32_i8((a), (b), (c))
+#define __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, x, y, z) ::sqemu::mfma_f32_32x32x8f16((a), (b), (c))
 #define __shfl_xor(v, m, w) ::sqemu::shfl_xor((v), (m), (w))
 
 template <typename T>

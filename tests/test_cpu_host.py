@@ -30,6 +30,19 @@ def test_every_declared_symbol_is_exported():
     assert not missing, missing
 
 
+def test_integration_binding_lists_every_declaration():
+    """The Rust -sys binding shown for maintainers binds every function the
+    header declares, and nothing else."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    declared = set(re.findall(r"\b(sq_[a-z0-9_]+)\s*\(", text))
+    doc = open(os.path.join(os.path.dirname(HEADER), "..", "INTEGRATION.md")).read()
+    block = doc[doc.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    bound = set(re.findall(r"pub fn (sq_[a-z0-9_]+)\(", block))
+    assert bound == declared, (sorted(declared - bound), sorted(bound - declared))
+
+
 def inspect(path):
     info = ModelInfo()
     inv = np.zeros(64, np.float32)

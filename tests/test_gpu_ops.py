@@ -131,7 +131,7 @@ def term_mag(x, w_f32):
 
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
 @pytest.mark.parametrize("k,n", SHAPES)
-@pytest.mark.parametrize("m", [1, 5, 67])
+@pytest.mark.parametrize("m", [1, 5, 67, 200])
 @pytest.mark.parametrize("f32_acts", [False, True])
 def test_linear_matches_oracle(wtype, k, n, m, f32_acts):
     if wtype == O.BF16 and f32_acts:
@@ -153,6 +153,31 @@ def test_linear_matches_oracle(wtype, k, n, m, f32_acts):
     # of |terms| <= mag is bounded by ~k*eps*mag; 4e-6 * mag covers k <= 8192
     # with the tree orders used on both sides.
     assert np.all(err <= 4e-6 * mag + 1e-6), float((err / (mag + 1e-30)).max())
+
+
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+def test_matmul_tiles_agree(wtype, monkeypatch):
+    """The prefill matmul's two tilings (64 x 64 on v_mfma_i32_16x16x32_i8,
+    128 x 128 on v_mfma_i32_32x32x32_i8) fold the same per-block terms in the
+    same order for every output, so without a K split they agree bit for
+    bit; the 128 x 128 result also matches the oracle (matmul.rs:133-171)."""
+    m, k, n = 1024, 2048, 4096      # 256 and 1024 tiles: neither kernel splits K
+    w, _ = quant_weights(wtype, n, k, seed=77 + wtype)
+    x = (rng(3).standard_normal((m, k)) * 1.5).astype(np.float32)
+    W = ops.Weight(wtype, w, n, k)
+    d_x = DeviceArray.from_numpy(x)
+    outs = {}
+    for tile in ("64", "128"):
+        monkeypatch.setenv("SQUIRREL_GEMM_TILE", tile)
+        out = DeviceArray((m, n))
+        ops.linear(d_x, W, out)
+        outs[tile] = out.numpy()
+    assert np.array_equal(outs["64"], outs["128"])
+    rows = np.arange(0, m, 97)
+    want = O.linear(x[rows], wtype, w, n, O.W8A8)
+    wf = np.stack([O.dequantize(wtype, w[i], k) for i in range(n)])
+    err = np.abs(outs["128"][rows].astype(np.float64) - want)
+    assert np.all(err <= 4e-6 * term_mag(x[rows], wf) + 1e-6)
 
 
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
