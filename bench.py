@@ -45,7 +45,10 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 # Matrix elements per layer of the 1B shape: QKV 2048x3072, o 2048x2048,
 # gate/up 2048x16384, down 8192x2048.
 MATMUL_ELEMS_PER_LAYER = 60817408
-VALU_RESCALE_OPS = 3        # per output element per 32-block in the int8 matmul: cvt, scale product, fma
+# per output element per 32-block in the int8 matmul: the convert of the
+# integer block sum and the fused multiply-add (the scale product comes from
+# the f16 matrix instruction)
+VALU_RESCALE_OPS = 2
 CONFIGS = {
     "q8": dict(wtype="Q8_0", prompt=32, gen=64,
                workload="Llama-3.2-1B arch, Q8_0 GGUF, 32-token prompt then 64 greedy tokens"),
@@ -235,7 +238,8 @@ def run_workload(name: str, cfg: dict, K: int, W: int, seed: int, kernel_iters: 
             "matmul_ops": mm_ops, "attention_flops": attn_flops}
         block["prefill_roofline"] = {"bound": "mfma", "achieved": round(mm_tops, 1), "peak": INT8_PEAK_TOPS,
                                      "unit": "TOP/s", "frac": round(mm_tops / INT8_PEAK_TOPS, 4),
-                                     "kernel": "gemm_mfma_kernel (int8 v_mfma_i32_16x16x32_i8)"}
+                                     "kernel": "gemm_mfma128_kernel (v_mfma_i32_32x32x32_i8, grids of 512+ "
+                                               "128x128 tiles) and gemm_mfma_kernel (v_mfma_i32_16x16x32_i8)"}
         log(f"[{name}] prefill phases {ph}; int8 matmul {mm_tops:.0f} TOP/s, attention {at_tflops:.1f} TFLOP/s")
     if kernel_iters and name == "q8":
         kernels = {}

@@ -48,6 +48,65 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(MatView table, const uint
 
 // rms_norm over rows (src/ops/rms_norm.rs:13-43); when act_q is non-null the
 // normed row is also quantized to Q8_0 (quantize_row_q8_0, dot_prod.rs:21-31).
+// Defined below the Q8_0 emitter it uses.
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, const float* w, int dim,
+                                                               float eps, float* out, int8_t* act_q,
+                                                               uint16_t* act_d);
+
+// quantize_row_q8_0 over n values (n a multiple of 32): one block per 32 lanes.
+__global__ __launch_bounds__(kBlock) void quantize_kernel(const float* x, size_t n, int8_t* qs,
+                                                           uint16_t* d) {
+    const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+    const bool vi = i < n;
+    const float v = vi ? x[i] : 0.0f;
+    float amax = fmaxf(sq_half_max(fabsf(v)), 0.0f);
+    float scale = sq_q8_scale(amax);
+    float inv = sq_q8_inv(scale);
+    if (vi) {
+        qs[i] = sq_q8_quant(v, inv);
+        if ((i & 31) == 0) d[i >> 5] = sq_f32_to_f16(scale);
+    }
+}
+
+// Q8_0 blocks of 8 consecutive values per thread (a lane quad holds a
+// block): the quantizer above with 16-byte loads and 8-byte stores.  All
+// values of one 32-element block are quantized with the same scale, so the
+// result is that of quantize_kernel.
+__device__ __forceinline__ void q8_emit8(const float* v, size_t g, bool valid, int8_t* qs, uint16_t* d) {
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(v[e]));
+    const float amax = fmaxf(sq_quad_max(m), 0.0f);
+    const float scale = sq_q8_scale(amax), inv = sq_q8_inv(scale);
+    if (valid) {
+        unsigned lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            lo |= (unsigned)(uint8_t)sq_q8_quant(v[e], inv) << (8 * e);
+            hi |= (unsigned)(uint8_t)sq_q8_quant(v[e + 4], inv) << (8 * e);
+        }
+        *(uint2*)(qs + 8 * g) = make_uint2(lo, hi);
+        if ((g & 3) == 0) d[g >> 2] = sq_f32_to_f16(scale);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void quantize8_kernel(const float* __restrict__ x, size_t n8,
+                                                            int8_t* __restrict__ qs, uint16_t* __restrict__ d) {
+    const size_t g = (size_t)blockIdx.x * kBlock + threadIdx.x;
+    const bool vg = g < n8;
+    float v[8] = {};
+    if (vg) {
+        const float4 a = ((const float4*)x)[2 * g], b = ((const float4*)x)[2 * g + 1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    q8_emit8(v, g, vg, qs, d);
+}
+
+// Rows whose width is a multiple of 8 (of 32 when quantized) and at most
+// 8 * kBlock take the vector path: thread t holds elements 8t..8t+7 (16-byte
+// loads; the lane quad of a 32-element block shares its maximum).  Other
+// widths keep one element per thread, read once when the row fits.
 __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, const float* w, int dim,
                                                                float eps, float* out, int8_t* act_q,
                                                                uint16_t* act_d) {
@@ -57,6 +116,39 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
     __shared__ float s_red[kBlock / 64];
     const int r = blockIdx.x;
     const float* xr = x + (size_t)r * dim;
+    auto row_rms = [&](float ss) {
+        ss = sq_wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < kBlock / 64; i++) tot += s_red[i];
+        return sqrtf(tot / (float)dim + eps);
+    };
+    if (dim % 8 == 0 && dim <= NC * kBlock && (act_q == nullptr || dim % 32 == 0) &&
+        (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0) {
+        const int t8 = 8 * threadIdx.x;
+        const bool vt = t8 < dim;
+        float xv[8] = {}, wv[8] = {};
+        if (vt) {
+            const float4 a = *(const float4*)(xr + t8), b = *(const float4*)(xr + t8 + 4);
+            const float4 c = *(const float4*)(w + t8), d = *(const float4*)(w + t8 + 4);
+            xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+            wv[0] = c.x; wv[1] = c.y; wv[2] = c.z; wv[3] = c.w; wv[4] = d.x; wv[5] = d.y; wv[6] = d.z; wv[7] = d.w;
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss += xv[e] * xv[e];
+        const float rms = row_rms(ss);
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) y[e] = vt ? (xv[e] * wv[e]) / rms : 0.0f;
+        if (vt && out) {
+            *(float4*)(out + (size_t)r * dim + t8) = make_float4(y[0], y[1], y[2], y[3]);
+            *(float4*)(out + (size_t)r * dim + t8 + 4) = make_float4(y[4], y[5], y[6], y[7]);
+        }
+        if (act_q) q8_emit8(y, ((size_t)r * dim + t8) / 8, vt, act_q, act_d);
+        return;
+    }
     const bool cached = dim <= NC * kBlock;
     float xv[NC], wv[NC];
     float ss = 0.0f;
@@ -73,12 +165,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
     } else {
         for (int i = threadIdx.x; i < dim; i += kBlock) ss += xr[i] * xr[i];
     }
-    ss = sq_wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < kBlock / 64; i++) tot += s_red[i];
-    const float rms = sqrtf(tot / (float)dim + eps);
+    const float rms = row_rms(ss);
     // dim is a multiple of 32 and the stride is a multiple of 64, so every
     // aligned 32-lane group holds one whole block.
     auto emit = [&](int i, float xi, float wi) {
@@ -109,19 +196,32 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float* x, co
     }
 }
 
-// quantize_row_q8_0 over n values (n a multiple of 32): one block per 32 lanes.
-__global__ __launch_bounds__(kBlock) void quantize_kernel(const float* x, size_t n, int8_t* qs,
-                                                           uint16_t* d) {
-    const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
-    const bool vi = i < n;
-    const float v = vi ? x[i] : 0.0f;
-    float amax = fmaxf(sq_half_max(fabsf(v)), 0.0f);
-    float scale = sq_q8_scale(amax);
-    float inv = sq_q8_inv(scale);
-    if (vi) {
-        qs[i] = sq_q8_quant(v, inv);
-        if ((i & 31) == 0) d[i >> 5] = sq_f32_to_f16(scale);
+// silu_mul_kernel with 8 consecutive FFN outputs per thread (ffn is a
+// multiple of 32, so a group never crosses a row).
+__global__ __launch_bounds__(kBlock) void silu_mul8_kernel(const float* __restrict__ gu, int ffn, size_t n8,
+                                                            float* __restrict__ out, int8_t* __restrict__ act_q,
+                                                            uint16_t* __restrict__ act_d) {
+    const size_t g = (size_t)blockIdx.x * kBlock + threadIdx.x;
+    const bool vg = g < n8;
+    float v[8] = {};
+    if (vg) {
+        const size_t i = 8 * g, m = i / ffn, j = i % ffn;
+        const float4* G = (const float4*)(gu + m * 2 * ffn + j);
+        const float4* U = (const float4*)(gu + m * 2 * ffn + ffn + j);
+        const float4 g0 = G[0], g1 = G[1], u0 = U[0], u1 = U[1];
+        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float sg = gv[e] * sq_sigmoid(gv[e]);
+            v[e] = sg * uv[e];
+        }
+        if (out) {
+            ((float4*)out)[2 * g] = make_float4(v[0], v[1], v[2], v[3]);
+            ((float4*)out)[2 * g + 1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
     }
+    if (act_q) q8_emit8(v, g, vg, act_q, act_d);
 }
 
 // Split payload/scale <-> GGUF 34-byte Q8_0 blocks (tensor.rs:10-15).
@@ -193,7 +293,9 @@ __global__ __launch_bounds__(kBlock) void rope_rows_kernel(float* t, int row_dim
 }
 
 // ffn: gate = silu(gate); act = gate * up (layers.rs:73-74), then Q8_0
-// blocks of act when act_q is non-null.  gu holds [gate | up] per row.
+// blocks of act when act_q is non-null; the f32 act goes to out when that is
+// non-null (the integer path only reads the blocks).  gu holds [gate | up]
+// per row.
 __global__ __launch_bounds__(kBlock) void silu_mul_kernel(const float* gu, int ffn, size_t n,
                                                            float* out, int8_t* act_q,
                                                            uint16_t* act_d) {
@@ -206,7 +308,7 @@ __global__ __launch_bounds__(kBlock) void silu_mul_kernel(const float* gu, int f
         const float u = gu[m * 2 * ffn + ffn + j];
         const float sg = g * sq_sigmoid(g);
         f = sg * u;
-        out[i] = f;
+        if (out) out[i] = f;
     }
     if (act_q) {
         float amax = fmaxf(sq_half_max(fabsf(f)), 0.0f);
@@ -428,6 +530,10 @@ int launch_rmsnorm_rows(hipStream_t s, const float* x, const float* w, int rows,
 }
 
 int launch_quantize_rows(hipStream_t s, const float* x, size_t n, int8_t* qs, uint16_t* d) {
+    if (n % 32 == 0 && ((uintptr_t)x & 15) == 0) {
+        hipLaunchKernelGGL(quantize8_kernel, dim3(grid_for(n / 8, kBlock)), dim3(kBlock), 0, s, x, n / 8, qs, d);
+        return check_launch("quantize");
+    }
     hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, x, n, qs, d);
     return check_launch("quantize");
 }
@@ -461,6 +567,11 @@ int launch_rope_rows_table(hipStream_t s, float* t, int rows, int row_dim, int h
 
 int launch_silu_mul_rows(hipStream_t s, const float* gu, int ffn, size_t n, float* out, int8_t* act_q,
                          uint16_t* act_d) {
+    if (ffn % 32 == 0 && ((uintptr_t)gu & 15) == 0 && ((uintptr_t)out & 15) == 0) {
+        hipLaunchKernelGGL(silu_mul8_kernel, dim3(grid_for(n / 8, kBlock)), dim3(kBlock), 0, s, gu, ffn, n / 8, out,
+                           act_q, act_d);
+        return check_launch("silu_mul");
+    }
     hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, gu, ffn, n, out,
                        act_q, act_d);
     return check_launch("silu_mul");

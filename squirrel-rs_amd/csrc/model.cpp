@@ -668,7 +668,8 @@ int run_prefill(sq_ctx* c, size_t n) {
                               false, c->p_split, kGemmSplitFloats)) ||
             (st = phase(2)))
             return st;
-        if ((st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, c->p_act, a8 ? c->p_aq : nullptr, c->p_ad)) ||
+        if ((st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, a8 ? nullptr : c->p_act, a8 ? c->p_aq : nullptr,
+                                       c->p_ad)) ||
             (a8 && (st = tap(l, 3, F))))
             return st;
         if ((st = phase(0)) ||

@@ -135,6 +135,13 @@ __device__ __forceinline__ float sq_half_max(float v) {
     return (threadIdx.x & 32) ? hi : lo;
 }
 
+// Maximum over each lane quad (every lane of the wavefront active): the
+// 32-element block of a thread that holds 8 consecutive elements.
+__device__ __forceinline__ float sq_quad_max(float v) {
+    v = fmaxf(v, sq_dpp<0xB1, 0xF>(v));  // quad_perm [1,0,3,2]
+    return fmaxf(v, sq_dpp<0x4E, 0xF>(v));  // quad_perm [2,3,0,1]
+}
+
 // The Q8_0 activation quantizer of the reference, for one element whose block
 // amax is known: quantize_row_q8_0_scalar (src/kernels/dot_prod.rs:21-31).
 // scale = amax/127 (IEEE division), inv = scale > 0 ? 1/scale : 0,

@@ -57,8 +57,9 @@ def models(emu, tmp_path_factory):
     return out
 
 
-def run(emu, args, timeout=600):
-    p = subprocess.run([emu, *map(str, args)], capture_output=True, text=True, env=ENV, timeout=timeout)
+def run(emu, args, timeout=600, env=None):
+    p = subprocess.run([emu, *map(str, args)], capture_output=True, text=True, env={**ENV, **(env or {})},
+                       timeout=timeout)
     assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-4000:]
     assert "AddressSanitizer" not in p.stderr
     steps = [(int(m[1]), float(m[2]), float(m[3]), int(m[4]), int(m[5]))
@@ -109,6 +110,16 @@ def test_long_prefill_in_bounds(emu, models):
     """70 prompt rows: the unsplit matrix-core matmul tiles (m >= 64) with
     a ragged 6-row tail, and two 64-query tiles of the prefill attention."""
     steps, out = run(emu, [models["Q8_0"], W8A8, MULTI_KERNEL, 70, 1, 1, 128])
+    assert len(steps) == 2 and all(rel <= 1e-6 and dev == ora for _, rel, _, dev, ora in steps), out
+    assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+def test_long_prefill_128_tiles_in_bounds(emu, models, wtype):
+    """The same prefill with every matmul on the 128 x 128 tiles
+    (SQUIRREL_GEMM_TILE=128): 70 of a tile's 128 rows exist, and the grids
+    split K over the workspace."""
+    steps, out = run(emu, [models[wtype], W8A8, MULTI_KERNEL, 70, 1, 1, 128], env={"SQUIRREL_GEMM_TILE": "128"})
     assert len(steps) == 2 and all(rel <= 1e-6 and dev == ora for _, rel, _, dev, ora in steps), out
     assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
 
