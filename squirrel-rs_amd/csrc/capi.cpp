@@ -206,6 +206,11 @@ int sq_ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* 
     return ctx_score(c, ids, n, burn, logp);
 }
 
+int sq_gemm_counters(int reset, uint64_t* out) {
+    gemm_counters(reset != 0, out);
+    return 0;
+}
+
 int sq_ctx_act_taps(sq_ctx* c, int enable) {
     if (!c) return set_error(SQ_ERR_ARG, "act_taps: null context");
     return ctx_set_taps(c, enable != 0);

@@ -9,6 +9,8 @@
 // instead of M times (the reference re-streams them per row,
 // src/kernels/matmul.rs:34).  Per-block arithmetic is the decode matvec's:
 // exact i32 block sums, term = (f32(isum) * sa) * sw.
+#include <atomic>
+
 #include "launch.h"
 
 namespace sq {
@@ -580,22 +582,50 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
     *o = accumulate ? *o + v : v;
 }
 
-// A grid of fewer than 256 tiles (short inputs, narrow matrices) splits K
-// over up to 512 workgroups when the workspace holds the partial tiles; the
-// partials are then summed in a fixed order, so results do not depend on
-// scheduling.
+// Compute units of the current device (the grid-size rules below are in
+// workgroups per CU).
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Matmul launches since the last reset (measurement aid): all, K-split,
+// 128 x 128 tiles, and the largest split count.
+std::atomic<uint64_t> g_launches{0}, g_split_launches{0}, g_tile128_launches{0}, g_max_splits{0};
+void count_launch(int splits, bool tile128) {
+    g_launches++;
+    if (splits > 1) g_split_launches++;
+    if (tile128) g_tile128_launches++;
+    uint64_t prev = g_max_splits.load();
+    while ((uint64_t)splits > prev && !g_max_splits.compare_exchange_weak(prev, (uint64_t)splits)) {
+    }
+}
+
+// A grid of fewer tiles than the device has CUs (short inputs, narrow
+// matrices) splits K over about two workgroups per CU when the workspace
+// holds the partial tiles; the partials are then summed in a fixed order, so
+// results do not depend on scheduling.
 template <int WT>
 int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
              bool acc, float* ws, size_t ws_floats) {
     const int gx = (w.rows + MQ_T - 1) / MQ_T, gy = (m + MQ_T - 1) / MQ_T;
     const int KB = w.k / 32, chunks = (KB + MQ_KB - 1) / MQ_KB;
+    const int cus = device_cus();
     int splits = 1;
-    if (ws != nullptr && gx * gy < 256) {
-        splits = min(chunks, (512 + gx * gy - 1) / (gx * gy));
+    if (ws != nullptr && gx * gy < cus) {
+        splits = min(chunks, (2 * cus + gx * gy - 1) / (gx * gy));
         while (splits > 1 && (size_t)splits * m * w.rows > ws_floats) splits--;
     }
     const int kbs = ((chunks + splits - 1) / splits) * MQ_KB;  // blocks per split
     splits = (KB + kbs - 1) / kbs;
+    count_launch(splits, false);
     hipError_t e;
     if (splits == 1) {
         hipLaunchKernelGGL(gemm_mfma_kernel<WT>, dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0,
@@ -614,26 +644,28 @@ int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
     return 0;
 }
 
-// 128 x 128 tiles.  They pay where the output alone gives at least 512 of
-// them (two workgroups on each CU, for example the gate/up projection of a
+// 128 x 128 tiles.  They pay where the output alone gives at least two of
+// them per CU (512 on MI355X; for example the gate/up projection of a
 // 2048-token prompt: 2048 tiles, 230 us against 265 us on 64 x 64 tiles);
 // smaller grids return 1 (nothing launched) and take the 64 x 64 kernel,
 // which holds four workgroups per CU (256 tiles of 128 x 128: 122 against
-// 92 us).  When pinned to this tiling, a grid of fewer than 512 workgroups
-// splits K while the workspace holds the partial tiles.
+// 92 us).  When pinned to this tiling, a grid of fewer than two workgroups
+// per CU splits K while the workspace holds the partial tiles.
 template <int WT>
 int run_mfma128(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
                 bool acc, float* ws, size_t ws_floats, bool force) {
     const int gx = (w.rows + M8_T - 1) / M8_T, gy = (m + M8_T - 1) / M8_T;
     const int KB = w.k / 32, chunks = (KB + M8_KB - 1) / M8_KB;
+    const int full = 2 * device_cus();
     int splits = 1;
-    if (ws != nullptr && gx * gy < 512) {
-        splits = min(chunks, (512 + gx * gy - 1) / (gx * gy));
+    if (ws != nullptr && gx * gy < full) {
+        splits = min(chunks, (full + gx * gy - 1) / (gx * gy));
         while (splits > 1 && (size_t)splits * m * w.rows > ws_floats) splits--;
     }
-    if (!force && gx * gy < 512) return 1;
+    if (!force && gx * gy < full) return 1;
     const int kbs = ((chunks + splits - 1) / splits) * M8_KB;
     splits = (KB + kbs - 1) / kbs;
+    count_launch(splits, true);
     hipError_t e;
     if (splits == 1) {
         hipLaunchKernelGGL(gemm_mfma128_kernel<WT>, dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0,
@@ -697,6 +729,21 @@ int dispatch(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
 }
 
 }  // namespace
+
+void gemm_counters(bool reset, uint64_t* out) {
+    if (out) {
+        out[0] = g_launches.load();
+        out[1] = g_split_launches.load();
+        out[2] = g_tile128_launches.load();
+        out[3] = g_max_splits.load();
+    }
+    if (reset) {
+        g_launches = 0;
+        g_split_launches = 0;
+        g_tile128_launches = 0;
+        g_max_splits = 0;
+    }
+}
 
 int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq, const uint16_t* ad,
                 const float* x, int m, float* out, int ldo, bool accumulate, float* ws, size_t ws_floats) {

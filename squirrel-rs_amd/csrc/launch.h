@@ -125,6 +125,9 @@ int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint3
 // ws: room for ws_floats floats of partial tiles, for a K split of the
 // integer path when the output has few tiles (null: no split).
 constexpr size_t kGemmSplitFloats = (size_t)4 << 20;
+// Integer matmul launches on the matrix cores since the last reset: out[0]
+// all, [1] with a K split, [2] on 128 x 128 tiles, [3] the largest split.
+void gemm_counters(bool reset, uint64_t* out);
 int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq,
                 const uint16_t* ad, const float* x, int m, float* out, int ldo, bool accumulate,
                 float* ws = nullptr, size_t ws_floats = 0);

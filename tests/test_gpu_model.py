@@ -196,11 +196,19 @@ def test_long_prefill_unsplit_matrix_core_tiles(tiny_gguf, wtype):
     256 output tiles (8 x 32 for the o and down projections), so they run on
     the matrix cores without the K split, accumulating the residual in place;
     shorter prompts take the split path."""
+    from sqhip import ops
     path = tiny_gguf(wtype, "g4")
     seq = teacher_seq(2048, n_prompt=2048, n_decode=2, seed=17)
+    ops.gemm_counters(reset=True)
     got, toks, (m, c, blocks) = run_gpu(path, seq, max_pos=2056)
+    n = ops.gemm_counters(reset=True)
+    assert n["launches"] == 4 * 2 and n["split_launches"] == 0, n   # 4 matmuls x 2 layers, none split
     rows = check_logits(path, seq, got, blocks, f"{wtype}/long prefill", max_pos=2056)
     assert len(rows) == 3
+    c.reset_cache()
+    c.forward(np.asarray(seq[0][:13]))
+    n = ops.gemm_counters(reset=True)
+    assert n["launches"] == 8 and n["split_launches"] == 8 and n["max_splits"] > 1, n  # a 13-token prompt splits
     for g, t in zip(got, toks):
         assert t == O.greedy(g)
 

@@ -170,7 +170,11 @@ def test_matmul_tiles_agree(wtype, monkeypatch):
     for tile in ("64", "128"):
         monkeypatch.setenv("SQUIRREL_GEMM_TILE", tile)
         out = DeviceArray((m, n))
+        ops.gemm_counters(reset=True)
         ops.linear(d_x, W, out)
+        got = ops.gemm_counters(reset=True)
+        assert got["launches"] == 1 and got["split_launches"] == 0, got
+        assert got["tile128_launches"] == (1 if tile == "128" else 0), got
         outs[tile] = out.numpy()
     assert np.array_equal(outs["64"], outs["128"])
     rows = np.arange(0, m, 97)
