@@ -255,6 +255,74 @@ def run_workload(name: str, cfg: dict, K: int, W: int, seed: int, kernel_iters: 
     return block
 
 
+# Stamps of the persistent step's timeline per layer (sq_ctx_step_trace), in
+# the order the critical path passes them; each phase ends at its stamp.
+TIMELINE_PHASES = [
+    ("hidden-row gather + norm (QKV input)", 0), ("QKV rows", 1), ("q -> attention -> attention output", 2),
+    ("tile merge", 3), ("attention-output gather (o input)", 4), ("o rows", 5),
+    ("hidden-row gather + norm (gate/up input)", 6), ("gate/up rows", 7), ("SiLU + Q8_0", 8),
+    ("FFN-activation gather (down input)", 9), ("down rows", 10)]
+
+
+def step_timeline(config: str, seed: int, steps: int = 4) -> int:
+    """Per-phase timeline of the persistent decode step: for every layer and
+    phase, the median over workgroups of the time from the workgroup's
+    previous stamp to the phase's stamp (the first phase starts at the
+    previous layer's down-rows stamp), averaged over the inner layers."""
+    import ctypes as C
+    import sqhip
+    from sqhip._lib import check, lib
+    cfg = CONFIGS[config]
+    path = model_path(cfg["wtype"], seed)
+    model = sqhip.Llama3_2(path)
+    S = cfg["prompt"]
+    ctx = model.new_context(S + 64)
+    if not ctx.persistent:
+        print("the persistent decode step does not serve this workload", file=sys.stderr)
+        return 2
+    khz = C.c_int()
+    check(lib().sq_device_wall_clock_khz(C.byref(khz)))
+    us_per_tick = 1e3 / khz.value
+    prompt = np.random.default_rng(seed).integers(0, model.info.vocab, S).astype(np.uint32)
+    ctx.forward(prompt)
+    tok = ctx.argmax()
+    for _ in range(4):
+        ctx.forward([tok])
+        tok = ctx.argmax()
+    ctx.step_trace(True)
+    L = model.info.n_layers
+    per = {name: [] for name, _ in TIMELINE_PHASES}
+    layer_us, step_us, head_us = [], [], []
+    for _ in range(steps):
+        ctx.forward([tok])
+        tok = ctx.argmax()
+        t = ctx.step_trace_read().astype(np.int64)
+        for l in range(1, L - 1):
+            base = 1 + 20 * l
+            prev = t[:, base - 20 + 10]
+            for name, j in TIMELINE_PHASES:
+                cur = t[:, base + j]
+                ok = (cur > 0) & (prev > 0)
+                if ok.any():
+                    per[name].append(float(np.median(cur[ok] - prev[ok])) * us_per_tick)
+                prev = np.where(cur > 0, cur, prev)
+            layer_us.append(float(np.median(t[:, base + 10] - t[:, base - 20 + 10])) * us_per_tick)
+        end = t[0, 3 + 20 * L]
+        step_us.append(float(end - t[:, 0].min()) * us_per_tick)
+        head_us.append(float(end - np.median(t[:, 1 + 20 * (L - 1) + 10])) * us_per_tick)
+    print(f"# Persistent decode step timeline: {cfg['workload']}, {steps} traced steps, layers 1-{L - 2}")
+    print()
+    print("| phase | median over workgroups, mean over layers (us) |")
+    print("|---|---:|")
+    for name, _ in TIMELINE_PHASES:
+        v = per[name]
+        print(f"| {name} | {np.mean(v):.2f} |" if v else f"| {name} | - |")
+    print(f"| **layer** (down rows to down rows) | **{np.mean(layer_us):.2f}** |")
+    print(f"| last layer's down rows to the token (final norm, LM head, argmax) | {np.mean(head_us):.2f} |")
+    print(f"| whole step (first workgroup start to the token) | {np.mean(step_us):.2f} |")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -269,6 +337,8 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--multi-kernel", action="store_true",
                     help="decode with one kernel per op (hipGraph) instead of the persistent step kernel")
+    ap.add_argument("--step-timeline", action="store_true",
+                    help="only print the persistent decode step's per-phase timeline for --config, then exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB five times (the known-size "
                          "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
@@ -280,6 +350,8 @@ def main() -> int:
 
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.step_timeline:
+        return step_timeline(args.config, args.seed)
     if args.config == "bf16":
         print("the BF16 workload's kernels (f32 activations) are switched off on the device", file=sys.stderr)
         return 2

@@ -141,6 +141,8 @@ int sq_ctx_decode_kernel(const sq_ctx* c);
  * _read copies the most recent step's stamps (grid * stride values); with
  * out == NULL it only reports grid and stride. */
 int sq_ctx_step_trace(sq_ctx* c, int enable);
+/* The current device's wall-clock rate in kHz (the unit of the step trace). */
+int sq_device_wall_clock_khz(int* khz);
 int sq_ctx_step_trace_read(sq_ctx* c, uint64_t* out, size_t n, int* grid, int* stride);
 size_t sq_ctx_seq_len(const sq_ctx* c);
 /* Quantized-activation taps (measurement and parity aid, no reference

@@ -195,6 +195,14 @@ int sq_ctx_step_trace_read(sq_ctx* c, uint64_t* out, size_t n, int* grid, int* s
 
 size_t sq_ctx_seq_len(const sq_ctx* c) { return c ? c->seq_len : 0; }
 
+int sq_device_wall_clock_khz(int* khz) {
+    if (!khz) return set_error(SQ_ERR_ARG, "wall_clock_khz: null argument");
+    int dev = 0;
+    SQ_HIP_CHECK(hipGetDevice(&dev));
+    SQ_HIP_CHECK(hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev));
+    return 0;
+}
+
 int sq_ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms) {
     if (!c || !ids || !ms) return set_error(SQ_ERR_ARG, "prefill_phases: null argument");
     if (n > c->max_pos) return set_error(SQ_ERR_CACHE_FULL, "prefill_phases: prompt longer than the context");

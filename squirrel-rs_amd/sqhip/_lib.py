@@ -86,6 +86,7 @@ PROTOS = {
     "sq_ctx_time_kernel": ([vp, i32, i32, C.POINTER(C.c_double), C.POINTER(C.c_uint64)], i32),
     "sq_ctx_score": ([vp, vp, sz, sz, vp], i32),
     "sq_gemm_counters": ([i32, vp], i32),
+    "sq_device_wall_clock_khz": ([vp], i32),
     "sq_log_softmax_at": ([vp, sz, u32, vp], i32),
     "sq_ctx_prefill_phases": ([vp, vp, sz, vp], i32),
 }
