@@ -143,11 +143,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 // Prefill attention on the matrix cores, f32 in and out
 // (v_mfma_f32_16x16x4_f32): 64 query rows of one head per workgroup, 16 per
 // wavefront; K and V tiles of 64 positions staged in LDS (V transposed);
-// online softmax per row.
+// online softmax per query.
 // MFMA operand layout (checked on the device): lane l supplies A[l % 16][l / 16]
 // and B[l / 16][l % 16]; result r of lane l is D[4 (l / 16) + r][l % 16].
-// The contraction index of step s is 16 (l / 16) + s, so that each lane's 16
-// operands of a 64-long contraction are contiguous in LDS (4 x 16-byte reads).
+// The scores are formed transposed, S^T = K Q^T: the key rows are the row
+// operand and the queries the column operand, with contraction index
+// 16 (l / 16) + s at step s, so each lane's 16 operands of the 64 dims are
+// contiguous in LDS.  Lane l then holds keys 4 (l / 16) + 0..3 of each
+// 16-key subtile for query l % 16, which is exactly the column operand of
+// O^T = V^T P^T when step s of a subtile takes key 4 (l / 16) + s: the
+// probabilities never leave the registers.  A query's scores sit in the four
+// lanes l % 16 + 16 j, so its maximum and sum are an in-lane fold plus two
+// lane exchanges.
 constexpr int PT = 64;       // queries and keys per tile
 constexpr int ALD = HD + 4;  // padded LDS row (floats)
 typedef float am_v4f __attribute__((ext_vector_type(4)));
@@ -171,9 +178,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
                                                             const float* __restrict__ vc, int pos0,
                                                             int m_rows, int n_heads, int n_kv_heads,
                                                             float* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) float s_k[PT][ALD];      // [key][dim]
-    __shared__ __attribute__((aligned(16))) float s_vt[HD][ALD];     // [dim][key]
-    __shared__ __attribute__((aligned(16))) float s_p[4][16][ALD];   // per wavefront: [row][key]
+    __shared__ __attribute__((aligned(16))) float s_k[PT][ALD];   // [key][dim]
+    __shared__ __attribute__((aligned(16))) float s_vt[HD][ALD];  // [dim][key]
 
     const int h = blockIdx.x;
     const int t0 = blockIdx.y * PT;
@@ -184,27 +190,24 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     const int li = lane & 15, lk = lane >> 4;
     const float scale = 1.0f / sqrtf((float)HD);
 
-    // this lane's query operands: row t0 + 16 wave + li, dims 16 lk .. 16 lk + 15
-    const int qrow = t0 + 16 * wave + li;
+    // this lane's query (t0 + 16 wave + li) and its dims 16 lk .. 16 lk + 15
+    const int tq = t0 + 16 * wave + li;
     float qa[16];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (qrow < m_rows) v = *(const float4*)(q + (size_t)qrow * q_dim + h * HD + 16 * lk + 4 * c);
+        if (tq < m_rows) v = *(const float4*)(q + (size_t)tq * q_dim + h * HD + 16 * lk + 4 * c);
         qa[4 * c] = v.x; qa[4 * c + 1] = v.y; qa[4 * c + 2] = v.z; qa[4 * c + 3] = v.w;
     }
-    // results of this lane: rows t0 + 16 wave + 4 lk + r, dims 16 dt + li
-    float mrow[4], lrow[4];
+    // online softmax state of query tq; o[dt][r] is O^T[16 dt + 4 lk + r][tq]
+    float mrow = -INFINITY, lrow = 0.0f;
     am_v4f o[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        mrow[r] = -INFINITY;
-        lrow[r] = 0.0f;
-        o[r] = am_v4f{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int dt = 0; dt < 4; dt++) o[dt] = am_v4f{0.f, 0.f, 0.f, 0.f};
 
     const int last_q = min(t0 + PT, m_rows) - 1;
     const int n_keys = pos0 + last_q + 1;  // keys any row of this tile can see
+    const int limit = pos0 + tq;           // query tq sees keys 0 ..= limit
     for (int k0 = 0; k0 < n_keys; k0 += PT) {
         __syncthreads();
         for (int e = tid; e < PT * HD / 4; e += 256) {
@@ -226,7 +229,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
         }
         __syncthreads();
 
-        // scores of 4 tiles of 16 keys: S[t] = Q K^T over the 64 dims
+        // S^T for 4 subtiles of 16 keys: sc[t][r] = score of key k0 + 16 t + 4 lk + r
         am_v4f sc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -236,70 +239,58 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
             for (int c = 0; c < 4; c++) {
                 const am_v4f k4 = *(const am_v4f*)(kr + 4 * c);
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * c + j], k4[j], acc, 0, 0, 0);
+                for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[j], qa[4 * c + j], acc, 0, 0, 0);
             }
             sc[t] = acc;
         }
-        // scale, causal mask (row t sees keys 0 ..= pos0 + t), online softmax
+        // scale, causal mask, online softmax (the four lanes of query tq
+        // hold its 64 scores)
+        float tmax = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int tq = t0 + 16 * wave + 4 * lk + r;
-            const int limit = pos0 + tq;
-            float rmax = -INFINITY;
+        for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int kk = k0 + 16 * t + li;
+            for (int r = 0; r < 4; r++) {
+                const int kk = k0 + 16 * t + 4 * lk + r;
                 sc[t][r] = (kk <= limit && tq < m_rows) ? sc[t][r] * scale : -INFINITY;
-                rmax = fmaxf(rmax, sc[t][r]);
+                tmax = fmaxf(tmax, sc[t][r]);
             }
-            rmax = row16_max(rmax);
-            const float mn = fmaxf(mrow[r], rmax);
-            const float alpha = (mrow[r] == -INFINITY) ? 0.0f : expf(mrow[r] - mn);
-            float rsum = 0.0f;
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mn = fmaxf(mrow, tmax);
+        const float alpha = (mrow == -INFINITY) ? 0.0f : expf(mrow - mn);
+        float rsum = 0.0f;
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
                 const float p = (sc[t][r] == -INFINITY) ? 0.0f : expf(sc[t][r] - mn);
-                s_p[wave][4 * lk + r][16 * t + li] = p;
+                sc[t][r] = p;
                 rsum += p;
             }
-            rsum = row16_sum(rsum);
-            lrow[r] = lrow[r] * alpha + rsum;
-            mrow[r] = mn;
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) o[dt][r] *= alpha;
-        }
-        // P back from LDS in the A layout (only this wavefront's lanes wrote it)
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_wave_barrier();
-        float pa[16];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const am_v4f p4 = *(const am_v4f*)&s_p[wave][li][16 * lk + 4 * c];
-            pa[4 * c] = p4[0]; pa[4 * c + 1] = p4[1]; pa[4 * c + 2] = p4[2]; pa[4 * c + 3] = p4[3];
-        }
-        // O[dt] += P V over the 64 keys
+        rsum += __shfl_xor(rsum, 16, 64);
+        rsum += __shfl_xor(rsum, 32, 64);
+        lrow = lrow * alpha + rsum;
+        mrow = mn;
+        // O^T[dt] = alpha O^T[dt] + V^T[16 dt + li][keys] P^T[keys][tq] over the 64 keys
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
-            const float* vr = &s_vt[16 * dt + li][16 * lk];
-            am_v4f acc = o[dt];
+            am_v4f acc = o[dt] * alpha;
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const am_v4f v4 = *(const am_v4f*)(vr + 4 * c);
+            for (int t = 0; t < 4; t++) {
+                const am_v4f v4 = *(const am_v4f*)&s_vt[16 * dt + li][16 * t + 4 * lk];
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[4 * c + j], v4[j], acc, 0, 0, 0);
+                for (int s = 0; s < 4; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[s], sc[t][s], acc, 0, 0, 0);
             }
             o[dt] = acc;
         }
-        // the P reads are done before the next tile's P stores
-        __builtin_amdgcn_wave_barrier();
     }
+    if (tq < m_rows) {
+        const float inv = 1.0f / lrow;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int tq = t0 + 16 * wave + 4 * lk + r;
-        if (tq >= m_rows) continue;
-        const float inv = 1.0f / lrow[r];
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++) out[(size_t)tq * q_dim + h * HD + 16 * dt + li] = o[dt][r] * inv;
+        for (int dt = 0; dt < 4; dt++) {
+            float* dst = out + (size_t)tq * q_dim + h * HD + 16 * dt + 4 * lk;
+            *(float4*)dst = make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+        }
     }
 }
 
