@@ -182,7 +182,17 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     __shared__ __attribute__((aligned(16))) float s_vt[HD][ALD];  // [dim][key]
 
     const int h = blockIdx.x;
-    const int t0 = blockIdx.y * PT;
+    // A query tile's work grows with its index (causal).  Workgroups are
+    // dispatched in order and the whole grid is resident at once, so the
+    // workgroups sharing a CU are a quarter of the grid apart; with quarters
+    // [0, B), [B, 2B), [2B, 3B), [3B, 4B) of the tile indices taken as a,
+    // 4B-1-a, B+a, 3B-1-a, every CU gets the same number of key tiles.
+    int ty = blockIdx.y;
+    if ((gridDim.y & 3) == 0) {
+        const int B = gridDim.y >> 2, k = ty / B, a = ty % B;
+        ty = k == 0 ? a : k == 1 ? 4 * B - 1 - a : k == 2 ? B + a : 3 * B - 1 - a;
+    }
+    const int t0 = ty * PT;
     const int g = h / (n_heads / n_kv_heads);
     const int q_dim = n_heads * HD;
     const int kv_dim = n_kv_heads * HD;
