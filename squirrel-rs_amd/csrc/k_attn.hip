@@ -173,7 +173,9 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
 }
 
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ q,
+// Three workgroups per CU: the registers of the next K/V tile's loads fit
+// there without spilling (at four, 128 registers, they spill).
+__global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __restrict__ q,
                                                             const float* __restrict__ kc,
                                                             const float* __restrict__ vc, int pos0,
                                                             int m_rows, int n_heads, int n_kv_heads,
@@ -183,10 +185,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
 
     const int h = blockIdx.x;
     // A query tile's work grows with its index (causal).  Workgroups are
-    // dispatched in order and the whole grid is resident at once, so the
-    // workgroups sharing a CU are a quarter of the grid apart; with quarters
-    // [0, B), [B, 2B), [2B, 3B), [3B, 4B) of the tile indices taken as a,
-    // 4B-1-a, B+a, 3B-1-a, every CU gets the same number of key tiles.
+    // dispatched in order; with quarters [0, B), [B, 2B), [2B, 3B), [3B, 4B)
+    // of the tile indices taken as a, 4B-1-a, B+a, 3B-1-a, workgroups a
+    // quarter of the grid apart carry equal work in sum, which balances the
+    // CUs when the grid is resident at once (four workgroups per CU) and
+    // interleaves cheap and costly tiles when it is dispatched in waves
+    // (measured equal to heaviest-first order there).
     int ty = blockIdx.y;
     if ((gridDim.y & 3) == 0) {
         const int B = gridDim.y >> 2, k = ty / B, a = ty % B;
@@ -218,31 +222,62 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     const int last_q = min(t0 + PT, m_rows) - 1;
     const int n_keys = pos0 + last_q + 1;  // keys any row of this tile can see
     const int limit = pos0 + tq;           // query tq sees keys 0 ..= limit
-    for (int k0 = 0; k0 < n_keys; k0 += PT) {
-        __syncthreads();
-        for (int e = tid; e < PT * HD / 4; e += 256) {
-            {   // K: thread e takes row e / 16, dims 4 (e % 16) ..
-                const int r = e >> 4, c4 = e & 15;
-                float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (k0 + r < n_keys) kv = *(const float4*)(kc + (size_t)(k0 + r) * kv_dim + g * HD + 4 * c4);
-                *(float4*)&s_k[r][4 * c4] = kv;
-            }
-            {   // V, transposed: thread e takes row e % 64, dims 4 (e / 64) ..
-                const int r = e & 63, c4 = e >> 6;
-                float4 vv = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (k0 + r < n_keys) vv = *(const float4*)(vc + (size_t)(k0 + r) * kv_dim + g * HD + 4 * c4);
-                s_vt[4 * c4][r] = vv.x;
-                s_vt[4 * c4 + 1][r] = vv.y;
-                s_vt[4 * c4 + 2][r] = vv.z;
-                s_vt[4 * c4 + 3][r] = vv.w;
-            }
-        }
-        __syncthreads();
 
+    // This thread's four 16-byte units of a K tile (row e / 16, dims
+    // 4 (e % 16) ..) and of a V tile (row e % 64, dims 4 (e / 64) ..) for
+    // e = tid + 256 i; rows past the last key read the last key and are
+    // zeroed.  A tile's loads are issued half an iteration before it is
+    // staged (K during the softmax and P.V, V during the next scores), so
+    // their latency is spent on work.
+    float4 kreg[4], vreg[4];
+    auto load_k = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
+            const bool ok = kb + r < n_keys;
+            const float4 v = *(const float4*)(kc + (size_t)(ok ? kb + r : n_keys - 1) * kv_dim + g * HD + 4 * c4);
+            kreg[i] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto load_v = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i, r = e & 63, c4 = e >> 6;
+            const bool ok = kb + r < n_keys;
+            const float4 v = *(const float4*)(vc + (size_t)(ok ? kb + r : n_keys - 1) * kv_dim + g * HD + 4 * c4);
+            vreg[i] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_k = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
+            *(float4*)&s_k[r][4 * c4] = kreg[i];
+        }
+    };
+    auto store_v = [&]() {  // transposed
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i, r = e & 63, c4 = e >> 6;
+            s_vt[4 * c4][r] = vreg[i].x;
+            s_vt[4 * c4 + 1][r] = vreg[i].y;
+            s_vt[4 * c4 + 2][r] = vreg[i].z;
+            s_vt[4 * c4 + 3][r] = vreg[i].w;
+        }
+    };
+    load_k(0);
+    load_v(0);
+    store_k();
+    __syncthreads();
+    for (int k0 = 0; k0 < n_keys; k0 += PT) {
+        const bool more = k0 + PT < n_keys;
         // S^T for 4 subtiles of 16 keys: sc[t][r] = score of key k0 + 16 t + 4 lk + r
         am_v4f sc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
+            // one subtile's operand reads at a time (hoisted together they
+            // would take 64 VGPRs)
+            asm volatile("" ::: "memory");
             const float* kr = &s_k[16 * t + li][16 * lk];
             am_v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -253,6 +288,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
             }
             sc[t] = acc;
         }
+        // this tile's V (s_vt was last read by the previous P.V, before the
+        // barrier that ended it); then the next tile's K rows are requested
+        store_v();
+        if (more) load_k(k0 + PT);
         // scale, causal mask, online softmax (the four lanes of query tq
         // hold its 64 scores)
         float tmax = -INFINITY;
@@ -281,9 +320,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
         rsum += __shfl_xor(rsum, 32, 64);
         lrow = lrow * alpha + rsum;
         mrow = mn;
+        __syncthreads();  // V staged; every wavefront is done with s_k
         // O^T[dt] = alpha O^T[dt] + V^T[16 dt + li][keys] P^T[keys][tq] over the 64 keys
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
+            asm volatile("" ::: "memory");
             am_v4f acc = o[dt] * alpha;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
@@ -293,6 +334,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
             }
             o[dt] = acc;
         }
+        if (more) {
+            store_k();
+            load_v(k0 + PT);
+        }
+        __syncthreads();  // the next K staged; every wavefront is done with s_vt
     }
     if (tq < m_rows) {
         const float inv = 1.0f / lrow;
