@@ -238,8 +238,9 @@ def run_workload(name: str, cfg: dict, K: int, W: int, seed: int, kernel_iters: 
             "matmul_ops": mm_ops, "attention_flops": attn_flops}
         block["prefill_roofline"] = {"bound": "mfma", "achieved": round(mm_tops, 1), "peak": INT8_PEAK_TOPS,
                                      "unit": "TOP/s", "frac": round(mm_tops / INT8_PEAK_TOPS, 4),
-                                     "kernel": "gemm_mfma128_kernel (v_mfma_i32_32x32x32_i8, grids of 512+ "
-                                               "128x128 tiles) and gemm_mfma_kernel (v_mfma_i32_16x16x32_i8)"}
+                                     "kernel": "gemm_mfma32_kernel (v_mfma_i32_32x32x32_i8 on 128x128 or "
+                                               "128x64 tiles, grids of 512+) and gemm_mfma_kernel "
+                                               "(v_mfma_i32_16x16x32_i8, smaller grids, K split)"}
         log(f"[{name}] prefill phases {ph}; int8 matmul {mm_tops:.0f} TOP/s, attention {at_tflops:.1f} TFLOP/s")
     if kernel_iters and name == "q8":
         kernels = {}

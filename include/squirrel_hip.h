@@ -276,8 +276,10 @@ int sq_ctx_time_kernel(sq_ctx* c, int which, int iters, double* mean_us, uint64_
 int sq_ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms);
 /* Matrix-core matmul launches in this process since the last reset
  * (measurement and test aid, no reference counterpart): out[0] all, [1] those
- * that split K over workgroups, [2] those on 128 x 128 tiles, [3] the largest
- * split count.  out may be null; reset != 0 zeroes the counters afterwards. */
+ * that split K over workgroups, [2] those on the full-rate kernel's 128 x 128
+ * tiles, [3] the largest split count, [4] those on the full-rate kernel's
+ * 128 x 64 tiles (out holds 5 values).  out may be null; reset != 0 zeroes the
+ * counters afterwards. */
 int sq_gemm_counters(int reset, uint64_t* out);
 
 #ifdef __cplusplus

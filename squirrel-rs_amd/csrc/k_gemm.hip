@@ -10,6 +10,7 @@
 // src/kernels/matmul.rs:34).  Per-block arithmetic is the decode matvec's:
 // exact i32 block sums, term = (f32(isum) * sa) * sw.
 #include <atomic>
+#include <cstring>
 
 #include "launch.h"
 
@@ -377,19 +378,19 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(MatView w, const int8_t*
 }
 
 // ---- 128 x 128 tiles on the 32 x 32 matrix instructions ----------------------
-// The same contraction with four times the output per workgroup, for inputs
-// of at least 128 rows.  v_mfma_i32_32x32x32_i8 (the full int8 rate of
-// gfx950; the 16 x 16 x 32 form runs at half of it) gives the exact i32 isum
-// of a 32 x 32 tile for one block: lane l supplies 16 bytes of row l % 32,
-// half l / 32 of the block, and the other operand alike.  The scale products
-// come from one v_mfma_f32_32x32x8_f16 per tile and block (lanes 0-31 hold
-// the row's block scales in k-slots 0-1, the others zeros; the column operand
-// of block b holds sw_b in slot b).  Result element r of lane l is row
-// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  Each of the four wavefronts
-// computes 64 x 64 (2 x 2 tiles).  K advances two blocks per chunk through
-// two LDS buffers with one barrier per chunk; every thread keeps two chunks'
-// global loads in registers, issued two chunks ahead of their use.
-constexpr int M8_T = 128;
+// The same contraction on v_mfma_i32_32x32x32_i8 (the full int8 rate of
+// gfx950; the 16 x 16 x 32 form runs at half of it), which gives the exact
+// i32 isum of a 32 x 32 tile for one block: lane l supplies 16 bytes of row
+// l % 32, half l / 32 of the block, and the other operand alike.  The scale
+// products come from one v_mfma_f32_32x32x8_f16 per tile and block (lanes
+// 0-31 hold the row's block scales in k-slots 0-1, the others zeros; the
+// column operand of block b holds sw_b in slot b).  Result element r of lane
+// l is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  A workgroup
+// computes BM x BN (128 x 128 or 128 x 64) as four wavefronts of
+// BM / 2 x BN / 2, that is (BM / 64) x (BN / 64) tiles of 32 x 32 each.  K
+// advances two blocks per chunk through two LDS buffers with one barrier per
+// chunk; every thread keeps two chunks' global loads in registers, issued two
+// chunks ahead of their use.
 constexpr int M8_KB = 2;           // blocks per chunk
 constexpr int M8_KC = M8_KB * 32;  // bytes per row per chunk
 constexpr int M8_LD = M8_KC + 16;  // LDS row stride: 16-byte reads of 8 consecutive rows cover all banks
@@ -397,40 +398,52 @@ constexpr int M8_LD = M8_KC + 16;  // LDS row stride: 16-byte reads of 8 consecu
 typedef int m8_v16i __attribute__((ext_vector_type(16)));
 typedef float m8_v16f __attribute__((ext_vector_type(16)));
 
+template <int BM, int BN>
 struct M8Loads {
-    sq_v4i a[2];  // activation pieces (row p / 4, 16-byte unit p % 4 for p = tid, tid + 256)
-    sq_v4i w[2];  // Q8_0: weight pieces as a[]; Q4_0: w[0] is one packed block
+    sq_v4i a[BM / 64];  // activation pieces (row p / 4, 16-byte unit p % 4 for p = tid + 256 q)
+    sq_v4i w[BN / 64];  // Q8_0: weight pieces as a[]; Q4_0: w[0] is one packed block
     uint16_t sa, sw;
     bool va, vw;  // the scales are in range (applied when staged)
 };
 
-template <int WT>
-__global__ __launch_bounds__(256, 2) void gemm_mfma128_kernel(MatView w, const int8_t* __restrict__ aq,
-                                                              const uint16_t* __restrict__ ad, int m_rows,
-                                                              float* __restrict__ out, int ldo, int accumulate,
-                                                              int kbs, size_t split_stride) {
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][M8_T * M8_LD];
-    __shared__ __attribute__((aligned(16))) int8_t sW[2][M8_T * M8_LD];
+// Wavefronts per SIMD: two (174 registers on 128 x 128 tiles, 192 on
+// 128 x 64; at three the 128 x 64 tiles spill).
+template <int BM, int BN>
+constexpr int m8_occupancy() { return 2; }
+
+template <int WT, int BM, int BN>
+__global__ __launch_bounds__(256, (m8_occupancy<BM, BN>())) void gemm_mfma32_kernel(
+    MatView w, const int8_t* __restrict__ aq, const uint16_t* __restrict__ ad, int m_rows,
+    float* __restrict__ out, int ldo, int accumulate, int kbs, size_t split_stride) {
+    static_assert(BM == 128 && (BN == 64 || BN == 128), "tiles of 128 x 128 or 128 x 64");
+    constexpr int SM = BM / 64, SN = BN / 64;  // 32 x 32 tiles per wavefront in M and N
+    constexpr int NT = SM * SN;
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * M8_LD];
+    __shared__ __attribute__((aligned(16))) int8_t sW[2][BN * M8_LD];
     // sSa[buf][row][slot]: the chunk's two block scales in slots 0-1; slots
-    // 2-3 and row M8_T stay zero.  sSw[buf][b][col]: sw_b in slot b.
-    __shared__ __attribute__((aligned(16))) uint16_t sSa[2][M8_T + 1][4];
-    __shared__ __attribute__((aligned(16))) uint16_t sSw[2][M8_KB][M8_T][4];
+    // 2-3 and row BM stay zero.  sSw[buf][b][col]: sw_b in slot b.
+    __shared__ __attribute__((aligned(16))) uint16_t sSa[2][BM + 1][4];
+    __shared__ __attribute__((aligned(16))) uint16_t sSw[2][M8_KB][BN][4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = w.k, KB = K >> 5;
-    const int m0 = blockIdx.y * M8_T, n0 = blockIdx.x * M8_T;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int kb_begin = blockIdx.z * kbs, kb_end = min(KB, kb_begin + kbs);
     out += blockIdx.z * split_stride;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
     const int fr = lane & 31, fh = lane >> 5;
+    // the scale each thread fetches and stages: row tid % T of block
+    // (tid / T) % 2 (with 64 columns threads 128-255 repeat threads 0-127)
+    const int ra_s = tid & (BM - 1), ba_s = (tid / BM) & 1;
+    const int rw_s = tid & (BN - 1), bw_s = (tid / BN) & 1;
 
-    // Clear what staging never writes (slots 2-3, row M8_T), so no clear can
+    // Clear what staging never writes (slots 2-3, row BM), so no clear can
     // land on a scale another thread has already staged; the first chunk's
     // barrier publishes both.
-    for (int i = tid; i < 2 * (M8_T + 1); i += 256) {
-        uint32_t* z = (uint32_t*)&sSa[i / (M8_T + 1)][i % (M8_T + 1)][0];
+    for (int i = tid; i < 2 * (BM + 1); i += 256) {
+        uint32_t* z = (uint32_t*)&sSa[i / (BM + 1)][i % (BM + 1)][0];
         z[1] = 0;
-        if (i % (M8_T + 1) == M8_T) z[0] = 0;
+        if (i % (BM + 1) == BM) z[0] = 0;
     }
 
     // Every thread issues the same loads for every chunk, without branches:
@@ -439,38 +452,48 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma128_kernel(MatView w, const i
     // acc and rows past the end are never stored.  With a fixed count of
     // loads per chunk the wait before staging one register set can leave the
     // other set's loads in flight.
-    auto fetch = [&](M8Loads& L, int kb0) {
+    auto fetch = [&](M8Loads<BM, BN>& L, int kb0) {
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
+        for (int q = 0; q < SM; q++) {
             const int p = tid + 256 * q, r = p >> 2, u = p & 3;
             const int kb = min(kb0 + (u >> 1), KB - 1);
-            const size_t ra = (size_t)min(m0 + r, m_rows - 1), rw = (size_t)min(n0 + r, w.rows - 1);
+            const size_t ra = (size_t)min(m0 + r, m_rows - 1);
             L.a[q] = *(const sq_v4i*)(aq + ra * K + kb * 32 + 16 * (u & 1));
-            if constexpr (WT == WT_Q8_0) L.w[q] = *(const sq_v4i*)((const int8_t*)w.qs + rw * K + kb * 32 + 16 * (u & 1));
         }
-        if constexpr (WT == WT_Q4_0) {
-            const int r = tid >> 1, kb = min(kb0 + (tid & 1), KB - 1);
+        if constexpr (WT == WT_Q8_0) {
+#pragma unroll
+            for (int q = 0; q < SN; q++) {
+                const int p = tid + 256 * q, r = p >> 2, u = p & 3;
+                const int kb = min(kb0 + (u >> 1), KB - 1);
+                const size_t rw = (size_t)min(n0 + r, w.rows - 1);
+                L.w[q] = *(const sq_v4i*)((const int8_t*)w.qs + rw * K + kb * 32 + 16 * (u & 1));
+            }
+        } else {
+            const int r = (tid >> 1) & (BN - 1), kb = min(kb0 + (tid & 1), KB - 1);
             L.w[0] = *(const sq_v4i*)((const uint8_t*)w.qs + (size_t)min(n0 + r, w.rows - 1) * (K / 2) + kb * 16);
         }
-        const int r = tid & 127, kb = kb0 + (tid >> 7), kbc = min(kb, KB - 1);
-        const uint16_t sa = ad[(size_t)min(m0 + r, m_rows - 1) * KB + kbc];
-        const uint16_t sw = w.scale[(size_t)min(n0 + r, w.rows - 1) * KB + kbc];
-        L.sa = sa;
-        L.sw = sw;
-        L.va = m0 + r < m_rows && kb < kb_end;
-        L.vw = n0 + r < w.rows && kb < kb_end;
+        const int kba = kb0 + ba_s, kbw = kb0 + bw_s;
+        L.sa = ad[(size_t)min(m0 + ra_s, m_rows - 1) * KB + min(kba, KB - 1)];
+        L.sw = w.scale[(size_t)min(n0 + rw_s, w.rows - 1) * KB + min(kbw, KB - 1)];
+        L.va = m0 + ra_s < m_rows && kba < kb_end;
+        L.vw = n0 + rw_s < w.rows && kbw < kb_end;
     };
-    auto stage = [&](const M8Loads& L, int buf) {
+    auto stage = [&](const M8Loads<BM, BN>& L, int buf) {
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
+        for (int q = 0; q < SM; q++) {
             const int p = tid + 256 * q, r = p >> 2, u = p & 3;
             *(sq_v4i*)(sA[buf] + r * M8_LD + 16 * u) = L.a[q];
-            if constexpr (WT == WT_Q8_0) *(sq_v4i*)(sW[buf] + r * M8_LD + 16 * u) = L.w[q];
         }
-        if constexpr (WT == WT_Q4_0) {
+        if constexpr (WT == WT_Q8_0) {
+#pragma unroll
+            for (int q = 0; q < SN; q++) {
+                const int p = tid + 256 * q, r = p >> 2, u = p & 3;
+                *(sq_v4i*)(sW[buf] + r * M8_LD + 16 * u) = L.w[q];
+            }
+        } else {
             // byte j holds element j (low nibble) and j + 16 (high nibble);
             // per byte, nibble - 8 as a signed byte (see gemm_mfma_kernel)
-            const int r = tid >> 1, b = tid & 1;
+            const int r = (tid >> 1) & (BN - 1), b = tid & 1;
             const unsigned wd[4] = {(unsigned)L.w[0].x, (unsigned)L.w[0].y, (unsigned)L.w[0].z, (unsigned)L.w[0].w};
             int lo[4], hi[4];
 #pragma unroll
@@ -481,36 +504,38 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma128_kernel(MatView w, const i
             *(sq_v4i*)(sW[buf] + r * M8_LD + 32 * b) = sq_v4i{lo[0], lo[1], lo[2], lo[3]};
             *(sq_v4i*)(sW[buf] + r * M8_LD + 32 * b + 16) = sq_v4i{hi[0], hi[1], hi[2], hi[3]};
         }
-        const int r = tid & 127, b = tid >> 7;
-        sSa[buf][r][b] = L.va ? L.sa : (uint16_t)0;
-        *(uint2*)&sSw[buf][b][r][0] = make_uint2(L.vw ? (unsigned)L.sw << (16 * b) : 0u, 0u);
+        // (with 64 columns threads 128-255 store what threads 0-127 store:
+        // the same values, fetched from the same places)
+        sSa[buf][ra_s][ba_s] = L.va ? L.sa : (uint16_t)0;
+        *(uint2*)&sSw[buf][bw_s][rw_s][0] = make_uint2(L.vw ? (unsigned)L.sw << (16 * bw_s) : 0u, 0u);
     };
 
-    m8_v16f acc[4];
+    m8_v16f acc[NT];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
 
     auto compute = [&](int buf) {
         const int8_t* A = sA[buf];
         const int8_t* W = sW[buf];
-        mq_v4h sa[2];
+        mq_v4h sa[SM];
 #pragma unroll
-        for (int i = 0; i < 2; i++) sa[i] = *(const mq_v4h*)&sSa[buf][fh == 0 ? wm + 32 * i + fr : M8_T][0];
+        for (int i = 0; i < SM; i++) sa[i] = *(const mq_v4h*)&sSa[buf][fh == 0 ? wm + 32 * i + fr : BM][0];
         // one block's operands at a time: the row and column fragments and
-        // the column scale operands of the 2 x 2 tiles
-        sq_v4i af[2], bf[2];
-        mq_v4h sw[2];
+        // the column scale operands of the SM x SN tiles
+        sq_v4i af[SM], bf[SN];
+        mq_v4h sw[SN];
         auto operands = [&](int b) {
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                af[i] = *(const sq_v4i*)(A + (wm + 32 * i + fr) * M8_LD + 32 * b + 16 * fh);
-                bf[i] = *(const sq_v4i*)(W + (wn + 32 * i + fr) * M8_LD + 32 * b + 16 * fh);
-                sw[i] = *(const mq_v4h*)&sSw[buf][b][wn + 32 * i + fr][0];
+            for (int i = 0; i < SM; i++) af[i] = *(const sq_v4i*)(A + (wm + 32 * i + fr) * M8_LD + 32 * b + 16 * fh);
+#pragma unroll
+            for (int j = 0; j < SN; j++) {
+                bf[j] = *(const sq_v4i*)(W + (wn + 32 * j + fr) * M8_LD + 32 * b + 16 * fh);
+                sw[j] = *(const mq_v4h*)&sSw[buf][b][wn + 32 * j + fr][0];
             }
         };
-        // Products for (block, tile) pairs k = 4 b + t, issued one pair ahead
+        // Products for (block, tile) pairs k = NT b + t, issued one pair ahead
         // of the pair being folded in.
         const m8_v16i izero = {};
         const m8_v16f fzero = {};
@@ -520,14 +545,14 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma128_kernel(MatView w, const i
         d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0], bf[0], izero, 0, 0, 0);
         sc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[0], sw[0], fzero, 0, 0, 0);
 #pragma unroll
-        for (int k = 0; k < 4 * M8_KB; k++) {
-            if (k + 1 < 4 * M8_KB) {
-                const int i = ((k + 1) >> 1) & 1, j = (k + 1) & 1;
-                if (((k + 1) & 3) == 0) operands((k + 1) >> 2);
+        for (int k = 0; k < NT * M8_KB; k++) {
+            if (k + 1 < NT * M8_KB) {
+                const int t1 = (k + 1) % NT, i = t1 / SN, j = t1 % SN;
+                if (t1 == 0) operands((k + 1) / NT);
                 d[(k + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], izero, 0, 0, 0);
                 sc[(k + 1) & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[i], sw[j], fzero, 0, 0, 0);
             }
-            const int t = k & 3;
+            const int t = k % NT;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 // the combine of the reference's aarch64 kernels (dot_prod.rs:189-252):
@@ -543,7 +568,7 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma128_kernel(MatView w, const i
     // The loop body is straight-line code over two chunks (an odd count gets
     // one chunk past kb_end, whose zero scales fold nothing), so the wait
     // before staging a set leaves the other set's loads in flight.
-    M8Loads L0, L1;
+    M8Loads<BM, BN> L0, L1;
     const int n_chunks = (kb_end - kb_begin + M8_KB - 1) / M8_KB;
     fetch(L0, kb_begin);
     fetch(L1, kb_begin + M8_KB);
@@ -558,11 +583,11 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma128_kernel(MatView w, const i
         compute(1);
     }
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int m = m0 + wm + 32 * (t >> 1) + 8 * (r >> 2) + 4 * fh + (r & 3);
-            const int n = n0 + wn + 32 * (t & 1) + fr;
+            const int m = m0 + wm + 32 * (t / SN) + 8 * (r >> 2) + 4 * fh + (r & 3);
+            const int n = n0 + wn + 32 * (t % SN) + fr;
             if (m < m_rows && n < w.rows) {
                 float* o = out + (size_t)m * ldo + n;
                 *o = accumulate ? *o + acc[t][r] : acc[t][r];
@@ -597,12 +622,16 @@ int device_cus() {
 }
 
 // Matmul launches since the last reset (measurement aid): all, K-split,
-// 128 x 128 tiles, and the largest split count.
-std::atomic<uint64_t> g_launches{0}, g_split_launches{0}, g_tile128_launches{0}, g_max_splits{0};
-void count_launch(int splits, bool tile128) {
+// full-rate 128 x 128 tiles, the largest split count, full-rate 128 x 64
+// tiles.
+std::atomic<uint64_t> g_launches{0}, g_split_launches{0}, g_tile128_launches{0}, g_max_splits{0},
+    g_tile128x64_launches{0};
+// bn: 0 for the 64 x 64 kernel, else the full-rate kernel's tile columns (64 or 128)
+void count_launch(int splits, int bn) {
     g_launches++;
     if (splits > 1) g_split_launches++;
-    if (tile128) g_tile128_launches++;
+    if (bn == 128) g_tile128_launches++;
+    if (bn == 64) g_tile128x64_launches++;
     uint64_t prev = g_max_splits.load();
     while ((uint64_t)splits > prev && !g_max_splits.compare_exchange_weak(prev, (uint64_t)splits)) {
     }
@@ -625,7 +654,7 @@ int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
     }
     const int kbs = ((chunks + splits - 1) / splits) * MQ_KB;  // blocks per split
     splits = (KB + kbs - 1) / kbs;
-    count_launch(splits, false);
+    count_launch(splits, 0);
     hipError_t e;
     if (splits == 1) {
         hipLaunchKernelGGL(gemm_mfma_kernel<WT>, dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0,
@@ -644,36 +673,39 @@ int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
     return 0;
 }
 
-// 128 x 128 tiles.  They pay where the output alone gives at least two of
-// them per CU (512 on MI355X; for example the gate/up projection of a
-// 2048-token prompt: 2048 tiles, 230 us against 265 us on 64 x 64 tiles);
-// smaller grids return 1 (nothing launched) and take the 64 x 64 kernel,
-// which holds four workgroups per CU (256 tiles of 128 x 128: 122 against
-// 92 us).  When pinned to this tiling, a grid of fewer than two workgroups
-// per CU splits K while the workspace holds the partial tiles.
-template <int WT>
-int run_mfma128(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
-                bool acc, float* ws, size_t ws_floats, bool force) {
-    const int gx = (w.rows + M8_T - 1) / M8_T, gy = (m + M8_T - 1) / M8_T;
+// The full-rate kernel.  Its tiles pay where the output alone gives at
+// least two workgroups per CU (512 on MI355X): 128 x 128 tiles for the
+// gate/up projection of a 2048-token prompt (2048 tiles), 128 x 64 tiles
+// where 128 x 128 ones are too few (its QKV, o and down projections: 768,
+// 512 and 512 tiles; 7.8 against 8.0 ms for all the prompt's matmuls with
+// those on the 64 x 64 kernel, whose 64 x 64 tiles on the full-rate
+// instruction measured 9.5 ms).  A smaller grid returns 1 (nothing launched)
+// and takes gemm_mfma_kernel with its K split.  When pinned to a tiling, a
+// grid of fewer than two workgroups per CU splits K while the workspace
+// holds the partial tiles.
+template <int WT, int BM, int BN>
+int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
+               bool acc, float* ws, size_t ws_floats, bool force) {
+    const int gx = (w.rows + BN - 1) / BN, gy = (m + BM - 1) / BM;
     const int KB = w.k / 32, chunks = (KB + M8_KB - 1) / M8_KB;
     const int full = 2 * device_cus();
+    if (!force && gx * gy < full) return 1;
     int splits = 1;
     if (ws != nullptr && gx * gy < full) {
         splits = min(chunks, (full + gx * gy - 1) / (gx * gy));
         while (splits > 1 && (size_t)splits * m * w.rows > ws_floats) splits--;
     }
-    if (!force && gx * gy < full) return 1;
     const int kbs = ((chunks + splits - 1) / splits) * M8_KB;
     splits = (KB + kbs - 1) / kbs;
-    count_launch(splits, true);
+    count_launch(splits, BN);
     hipError_t e;
     if (splits == 1) {
-        hipLaunchKernelGGL(gemm_mfma128_kernel<WT>, dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo, acc ? 1 : 0,
-                           KB, (size_t)0);
+        hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo,
+                           acc ? 1 : 0, KB, (size_t)0);
     } else {
         const size_t stride = (size_t)m * w.rows;
-        hipLaunchKernelGGL(gemm_mfma128_kernel<WT>, dim3(gx, gy, splits), dim3(256), 0, s, w, aq, ad, m, ws, w.rows,
-                           0, kbs, stride);
+        hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy, splits), dim3(256), 0, s, w, aq, ad, m, ws,
+                           w.rows, 0, kbs, stride);
         e = hipGetLastError();
         if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
         hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
@@ -684,20 +716,30 @@ int run_mfma128(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_
     return 0;
 }
 
-// SQUIRREL_GEMM_TILE=64 or 128 pins the prefill matmul's tile (a test and
-// measurement aid); unset, inputs of at least 128 rows take the 128 x 128
-// kernel when its grid fills the device.
+// SQUIRREL_GEMM_TILE pins the prefill matmul's kernel (a test and
+// measurement aid): "64" the 64 x 64 kernel, "128x64" and "128" the
+// full-rate kernel on 128 x 64 or 128 x 128 tiles.  Unset, the largest
+// full-rate tiling whose grid fills the device is taken.
+enum : int { TILE_AUTO = 0, TILE_64 = 1, TILE_128X64 = 2, TILE_128 = 3 };
 int gemm_tile_override() {
     const char* e = getenv("SQUIRREL_GEMM_TILE");
-    return e ? atoi(e) : 0;
+    if (!e) return TILE_AUTO;
+    if (!strcmp(e, "64")) return TILE_64;
+    if (!strcmp(e, "128x64")) return TILE_128X64;
+    if (!strcmp(e, "128")) return TILE_128;
+    return TILE_AUTO;
 }
 
 template <int WT>
 int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
                 bool acc, float* ws, size_t ws_floats) {
     const int tile = gemm_tile_override();
-    if (tile != 64 && (m >= M8_T || tile == 128)) {
-        const int st = run_mfma128<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == 128);
+    if (tile == TILE_128 || (tile == TILE_AUTO && m >= 128)) {
+        const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128);
+        if (st != 1) return st;
+    }
+    if (tile == TILE_128X64 || (tile == TILE_AUTO && m >= 128)) {
+        const int st = run_mfma32<WT, 128, 64>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128X64);
         if (st != 1) return st;
     }
     return run_mfma<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats);
@@ -736,12 +778,14 @@ void gemm_counters(bool reset, uint64_t* out) {
         out[1] = g_split_launches.load();
         out[2] = g_tile128_launches.load();
         out[3] = g_max_splits.load();
+        out[4] = g_tile128x64_launches.load();
     }
     if (reset) {
         g_launches = 0;
         g_split_launches = 0;
         g_tile128_launches = 0;
         g_max_splits = 0;
+        g_tile128x64_launches = 0;
     }
 }
 

@@ -114,12 +114,13 @@ def test_long_prefill_in_bounds(emu, models):
     assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
 
 
+@pytest.mark.parametrize("tile", ["128", "128x64"])
 @pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
-def test_long_prefill_128_tiles_in_bounds(emu, models, wtype):
-    """The same prefill with every matmul on the 128 x 128 tiles
-    (SQUIRREL_GEMM_TILE=128): 70 of a tile's 128 rows exist, and the grids
-    split K over the workspace."""
-    steps, out = run(emu, [models[wtype], W8A8, MULTI_KERNEL, 70, 1, 1, 128], env={"SQUIRREL_GEMM_TILE": "128"})
+def test_long_prefill_full_rate_tiles_in_bounds(emu, models, wtype, tile):
+    """The same prefill with every matmul on the full-rate kernel's 128 x 128
+    or 128 x 64 tiles (SQUIRREL_GEMM_TILE=128 / 128x64): 70 of a tile's 128
+    rows exist, and the grids split K over the workspace."""
+    steps, out = run(emu, [models[wtype], W8A8, MULTI_KERNEL, 70, 1, 1, 128], env={"SQUIRREL_GEMM_TILE": tile})
     assert len(steps) == 2 and all(rel <= 1e-6 and dev == ora for _, rel, _, dev, ora in steps), out
     assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
 

@@ -157,17 +157,18 @@ def test_linear_matches_oracle(wtype, k, n, m, f32_acts):
 
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
 def test_matmul_tiles_agree(wtype, monkeypatch):
-    """The prefill matmul's two tilings (64 x 64 on v_mfma_i32_16x16x32_i8,
-    128 x 128 on v_mfma_i32_32x32x32_i8) fold the same per-block terms in the
-    same order for every output, so without a K split they agree bit for
-    bit; the 128 x 128 result also matches the oracle (matmul.rs:133-171)."""
-    m, k, n = 1024, 2048, 4096      # 256 and 1024 tiles: neither kernel splits K
+    """The prefill matmul's three tilings (64 x 64 on v_mfma_i32_16x16x32_i8,
+    128 x 64 and 128 x 128 on v_mfma_i32_32x32x32_i8) fold the same per-block
+    terms in the same order for every output, so without a K split they agree
+    bit for bit; the 128 x 128 result also matches the oracle
+    (matmul.rs:133-171)."""
+    m, k, n = 1024, 2048, 4096      # 1024, 512 and 256 tiles: no kernel splits K
     w, _ = quant_weights(wtype, n, k, seed=77 + wtype)
     x = (rng(3).standard_normal((m, k)) * 1.5).astype(np.float32)
     W = ops.Weight(wtype, w, n, k)
     d_x = DeviceArray.from_numpy(x)
     outs = {}
-    for tile in ("64", "128"):
+    for tile in ("64", "128x64", "128"):
         monkeypatch.setenv("SQUIRREL_GEMM_TILE", tile)
         out = DeviceArray((m, n))
         ops.gemm_counters(reset=True)
@@ -175,8 +176,10 @@ def test_matmul_tiles_agree(wtype, monkeypatch):
         got = ops.gemm_counters(reset=True)
         assert got["launches"] == 1 and got["split_launches"] == 0, got
         assert got["tile128_launches"] == (1 if tile == "128" else 0), got
+        assert got["tile128x64_launches"] == (1 if tile == "128x64" else 0), got
         outs[tile] = out.numpy()
     assert np.array_equal(outs["64"], outs["128"])
+    assert np.array_equal(outs["128x64"], outs["128"])
     rows = np.arange(0, m, 97)
     want = O.linear(x[rows], wtype, w, n, O.W8A8)
     wf = np.stack([O.dequantize(wtype, w[i], k) for i in range(n)])
