@@ -1,15 +1,16 @@
 #!/usr/bin/env python3
 """Benchmark: batch-1 prefill + greedy decode of the Llama-3.2-1B-shaped model.
 
-`python bench.py [--gpus 1] [--steps K] [--warmup W] [--config q8|q4|long|prefill] [--only]`
+`python bench.py [--gpus 1] [--steps K] [--warmup W] [--config q8|q4|q8_q4|long|prefill] [--only]`
 
 The headline is the Q8_0 workload (32-token prompt, then greedy tokens): a
 step is one decode token (forward + greedy sample), timed with HIP events on
 the context stream; the prompt's prefill is step 0 and is reported separately
 as prefill tok/s (the reference's convention: decode throughput excludes step
 1, scripts/bench.py:68-71).  Unless --only is given, the same run then
-measures the other workloads -- Q4_0 (128 + 256), a 4096-position context
-(+128) and a 2048-token batched prefill (+16) -- each in its own block of
+measures the other workloads -- Q4_0 (128 + 256, and the same on the Q8_0
+weights), a 4096-position context (+128) and a 2048-token batched prefill
+(+16) -- each in its own block of
 `configs` with its own roofline.  The BF16 workload is reported as not run
 (its kernels are switched off on the device).  Weights are random-init from a
 fixed seed (synthetic data; no checkpoint is available).
@@ -54,6 +55,9 @@ CONFIGS = {
                workload="Llama-3.2-1B arch, Q8_0 GGUF, 32-token prompt then 64 greedy tokens"),
     "q4": dict(wtype="Q4_0", prompt=128, gen=256,
                workload="Llama-3.2-1B arch, Q4_0 GGUF, 128-token prompt then 256 greedy tokens"),
+    # the Q4_0 workload on Q8_0 weights: the two weight types at the same positions
+    "q8_q4": dict(wtype="Q8_0", prompt=128, gen=256,
+                  workload="Llama-3.2-1B arch, Q8_0 GGUF, 128-token prompt then 256 greedy tokens"),
     "bf16": dict(wtype="BF16", prompt=128, gen=256,
                  workload="Llama-3.2-1B arch, BF16 GGUF, 128-token prompt then 256 greedy tokens"),
     "long": dict(wtype="Q8_0", prompt=4096, gen=128,
@@ -365,7 +369,7 @@ def main() -> int:
 
     configs = {}
     if not args.only:
-        for name in ("q8", "q4", "long", "prefill"):
+        for name in ("q8", "q4", "q8_q4", "long", "prefill"):
             if name == args.config:
                 continue
             c = CONFIGS[name]
@@ -373,6 +377,10 @@ def main() -> int:
             for k in ("_info", "_path", "_prompt"):
                 blk.pop(k)
             configs[name] = blk
+        if "q4" in configs and "q8_q4" in configs:
+            # Q4_0 against Q8_0 at the same positions (decode tok/s ratio)
+            configs["q4"]["vs_q8_same_workload"] = round(
+                configs["q4"]["decode_tok_s"] / configs["q8_q4"]["decode_tok_s"], 4)
         configs["bf16"] = {"workload": CONFIGS["bf16"]["workload"], "status": "not run",
                            "reason": "the f32-activation kernels (BF16 weights) are switched off on the device"}
 
