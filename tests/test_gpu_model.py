@@ -252,6 +252,31 @@ def test_persistent_deterministic_across_resets(tiny_gguf):
     assert np.array_equal(l1, l2) and np.array_equal(l1, l3)
 
 
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+def test_step_instances_agree(tiny_gguf, wtype):
+    """The persistent step is built twice: with the measurement and test
+    outputs (activation taps, per-workgroup timeline) and without them, the
+    instance ordinary decoding runs.  The phase-locked parity tests run the
+    first; both must compute the same tokens, bit for bit, here over one and
+    then two 64-position tiles (the chunk merge)."""
+    path = tiny_gguf(wtype, "g4")
+    seq = teacher_seq(2048, n_prompt=60, n_decode=8, seed=23)   # positions 61 .. 68
+    lean, lean_toks, _ = run_gpu(path, seq, max_pos=128, taps=False)
+    tapped, tapped_toks, _ = run_gpu(path, seq, max_pos=128, taps=True)
+    m = sq.Llama3_2(path)
+    c = m.new_context(128)
+    assert c.persistent
+    c.step_trace(True)
+    traced = []
+    for ids in [seq[0]] + [[t] for t in seq[1:]]:
+        c.forward(ids)
+        traced.append(c.logits())
+    assert lean_toks == tapped_toks
+    for step, (a, b, t) in enumerate(zip(lean, tapped, traced)):
+        assert np.array_equal(a, b), f"step {step}: taps change the logits"
+        assert np.array_equal(a, t), f"step {step}: the timeline changes the logits"
+
+
 def test_persistent_matches_multi_kernel_generation(tiny_gguf):
     """Greedy generations of the two decode paths agree token for token
     until a step whose top-2 margin is within rounding noise."""
