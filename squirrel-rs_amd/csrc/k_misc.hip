@@ -23,7 +23,9 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(MatView table, const uint
                                                         int dim, float* out) {
     const int t = blockIdx.x;
     uint32_t tok = tokens[t];
-    if ((int)tok >= table.rows) tok = table.rows - 1;  // ids are validated on the host
+    // ids are validated on the host; the unsigned compare also catches
+    // values of 2^31 and more, which a signed one would let through
+    if (tok >= (uint32_t)table.rows) tok = table.rows - 1;
     const int KB = dim >> 5;
     float* o = out + (size_t)t * dim;
     for (int e = threadIdx.x; e < dim; e += kBlock) {

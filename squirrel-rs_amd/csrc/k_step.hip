@@ -826,7 +826,7 @@ enum TraceSlot : int {
 // INSTR: the optional measurement and test outputs (the per-workgroup
 // timeline, the activation taps) are compiled in.  A launch that asks for
 // neither runs the instance without them, whose code the compiler lays out
-// better (measured 2% faster per token).
+// better (measured about 3.5% faster per token).
 template <int WT, bool INSTR>
 __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     __shared__ StepShared S;

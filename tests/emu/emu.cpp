@@ -8,6 +8,8 @@
 #include <chrono>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
+#include <map>
 #include <vector>
 
 #if defined(__has_feature)
@@ -328,6 +330,72 @@ void submit(Task t) {
 
 }  // namespace sqemu
 
+namespace sqemu {
+// Live device allocations (hipMalloc, hipHostMalloc, device symbols): base -> bytes.
+std::map<uintptr_t, size_t> g_dev;
+
+namespace {
+// The allocation that holds address a (one past the end counts), or none.
+const std::pair<const uintptr_t, size_t>* dev_block(uintptr_t a, size_t n = 0) {
+    auto it = g_dev.upper_bound(a);
+    if (it == g_dev.begin()) return nullptr;
+    --it;
+    return a + n <= it->first + it->second ? &*it : nullptr;
+}
+
+// Where a host address lies, or nullptr when it is no host memory: the
+// sanitizer's heap, stack and globals, else a mapping of /proc/self/maps
+// (file mappings such as the model file; the sanitizer's shadow regions,
+// which span terabytes, excluded).
+const char* host_region(uintptr_t a) {
+#ifdef SQEMU_ASAN
+    char name[64];
+    void* base = nullptr;
+    size_t size = 0;
+    const char* kind = __asan_locate_address((void*)a, name, sizeof name, &base, &size);
+    if (!strcmp(kind, "heap") || !strcmp(kind, "stack") || !strcmp(kind, "stack-fake") || !strcmp(kind, "global"))
+        return kind;
+#endif
+    FILE* f = fopen("/proc/self/maps", "r");
+    if (!f) return nullptr;
+    unsigned long lo, hi;
+    char line[512];
+    const char* found = nullptr;
+    while (!found && fgets(line, sizeof line, f)) {
+        if (sscanf(line, "%lx-%lx", &lo, &hi) == 2 && a >= lo && a < hi && hi - lo < (1ull << 40)) found = "mapping";
+    }
+    fclose(f);
+    return found;
+}
+}  // namespace
+
+void check_kernel_arg(const void* kernel, int index, const void* arg, size_t bytes) {
+    for (size_t off = 0; off + 8 <= bytes; off += 8) {
+        uint64_t w;
+        memcpy(&w, (const char*)arg + off, 8);
+        if (w < 4096 || w >= (1ull << 47) || dev_block(w)) continue;
+        if (const char* where = host_region(w)) {
+            char fn[256] = "?";
+#ifdef SQEMU_ASAN
+            // (the symbolizer takes return addresses: one byte into the entry)
+            __sanitizer_symbolize_pc((char*)const_cast<void*>(kernel) + 1, "%f", fn, sizeof fn);
+#endif
+            fatal("kernel %s (%p) argument %d (bytes %zu-%zu) holds 0x%lx, in host memory (%s) outside every live "
+                  "device allocation",
+                  fn, kernel, index, off, off + 7, (unsigned long)w, where);
+        }
+    }
+}
+
+void check_copy(const char* what, const void* d, const void* s, size_t n, hipMemcpyKind k) {
+    if (!n) return;
+    const bool dd = k == hipMemcpyDeviceToDevice || k == hipMemcpyHostToDevice;
+    const bool sd = k == hipMemcpyDeviceToDevice || k == hipMemcpyDeviceToHost;
+    if (dd && !dev_block((uintptr_t)d, n)) fatal("%s: destination %p (+%zu) is no device allocation", what, d, n);
+    if (sd && s && !dev_block((uintptr_t)s, n)) fatal("%s: source %p (+%zu) is no device allocation", what, s, n);
+}
+}  // namespace sqemu
+
 // ------------------------------------------------------------------ runtime API
 struct sqemu_stream {
     int dummy;
@@ -369,30 +437,36 @@ hipError_t hipMalloc(void** p, size_t n) {
     // device memory starts with arbitrary contents
     memset(q, 0xA5, n ? n : 1);
     *p = q;
+    sqemu::g_dev[(uintptr_t)q] = n;
     return hipSuccess;
 }
 hipError_t hipFree(void* p) {
+    if (p && !sqemu::g_dev.erase((uintptr_t)p)) sqemu::fatal("hipFree of %p, not a device allocation", p);
     free(p);
     return hipSuccess;
 }
 hipError_t hipHostMalloc(void** p, size_t n, unsigned) { return hipMalloc(p, n); }
 hipError_t hipHostFree(void* p) { return hipFree(p); }
-hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) {
+hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind k) {
+    sqemu::check_copy("hipMemcpy", d, s, n, k);
     if (n) memcpy(d, s, n);
     return hipSuccess;
 }
-hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind, hipStream_t) {
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t) {
     sqemu::submit([=]() {
+        sqemu::check_copy("hipMemcpyAsync", d, s, n, k);
         if (n) memmove(d, s, n);
     });
     return hipSuccess;
 }
 hipError_t hipMemset(void* d, int v, size_t n) {
+    sqemu::check_copy("hipMemset", d, nullptr, n, hipMemcpyHostToDevice);
     if (n) memset(d, v, n);
     return hipSuccess;
 }
 hipError_t hipMemsetAsync(void* d, int v, size_t n, hipStream_t) {
     sqemu::submit([=]() {
+        sqemu::check_copy("hipMemsetAsync", d, nullptr, n, hipMemcpyHostToDevice);
         if (n) memset(d, v, n);
     });
     return hipSuccess;
@@ -456,5 +530,13 @@ hipError_t hipGraphDestroy(hipGraph_t g) {
 }
 hipError_t hipGetSymbolAddress(void** p, const void* sym) {
     *p = const_cast<void*>(sym);
+    size_t bytes = 1;
+#ifdef SQEMU_ASAN
+    char name[64];
+    void* base = nullptr;
+    size_t size = 0;
+    if (!strcmp(__asan_locate_address(*p, name, sizeof name, &base, &size), "global") && base == *p) bytes = size;
+#endif
+    sqemu::g_dev[(uintptr_t)*p] = bytes;
     return hipSuccess;
 }

@@ -342,10 +342,23 @@ inline T max(T a, T b) { return a < b ? b : a; }
 
 // ------------------------------------------------------------------ kernel launch
 namespace sqemu {
+// Device memory on the GPU is its own address range; here it is host memory.
+// Every 8-byte word of every kernel argument is checked when the launch runs
+// (also on each graph replay): a word that points into host memory (heap,
+// stack, globals, file mappings) outside every live device allocation is a
+// host or freed pointer handed to a kernel, which the device could not
+// dereference, and stops the run.
+void check_kernel_arg(const void* kernel, int index, const void* arg, size_t bytes);
 template <typename... P, typename... A>
 void launch(void (*k)(P...), dim3 grid, dim3 block, size_t shm, hipStream_t, A&&... args) {
     auto tup = std::make_tuple(static_cast<std::decay_t<P>>(args)...);
     submit([=]() {
+        std::apply(
+            [&](const auto&... a) {
+                int i = 0;
+                (check_kernel_arg(reinterpret_cast<const void*>(k), i++, &a, sizeof(a)), ...);
+            },
+            tup);
         run_grid(grid, block, shm, [&]() { std::apply(k, tup); });
     });
 }

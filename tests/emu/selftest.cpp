@@ -2,7 +2,10 @@
 // TEST INFRASTRUCTURE ONLY.  `selftest oob` launches a kernel that reads one
 // element past a device buffer (the sanitizer must stop it); `selftest
 // diverge` calls a cross-lane operation from half a wavefront (the emulator
-// must abort); `selftest ok` runs the in-bounds twin and prints the sum.
+// must abort); `selftest host` hands the kernel a host array, `selftest
+// hoststruct` a struct holding one, and `selftest freed` replays a captured
+// launch whose buffer was freed after the capture (each must be refused);
+// `selftest ok` runs the in-bounds twin and prints the sum.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -13,6 +16,15 @@ __global__ void read_kernel(const float* x, int n, int extra, float* out) {
     for (int i = threadIdx.x; i < n + extra; i += 64) v += x[i];
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     if (threadIdx.x == 0) *out = v;
+}
+
+struct View {
+    const float* x;
+    int n;
+};
+
+__global__ void view_kernel(View v, float* out) {
+    if (threadIdx.x == 0) *out = v.x[0] + (float)v.n;
 }
 
 __global__ void diverge_kernel(float* out) {
@@ -32,6 +44,25 @@ int main(int argc, char** argv) {
     hipMemcpy(x, h, sizeof(h), hipMemcpyHostToDevice);
     if (!strcmp(what, "diverge")) {
         hipLaunchKernelGGL(diverge_kernel, dim3(1), dim3(64), 0, nullptr, out);
+    } else if (!strcmp(what, "host")) {
+        hipLaunchKernelGGL(read_kernel, dim3(1), dim3(64), 0, nullptr, (const float*)h, n, 0, out);
+    } else if (!strcmp(what, "hoststruct")) {
+        hipLaunchKernelGGL(view_kernel, dim3(1), dim3(64), 0, nullptr, View{h, n}, out);
+    } else if (!strcmp(what, "freed")) {
+        float* tmp = nullptr;
+        hipMalloc(&tmp, n * sizeof(float));
+        hipMemcpy(tmp, h, sizeof(h), hipMemcpyHostToDevice);
+        hipStream_t s;
+        hipStreamCreate(&s);
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        hipStreamBeginCapture(s, hipStreamCaptureModeGlobal);
+        hipLaunchKernelGGL(read_kernel, dim3(1), dim3(64), 0, s, (const float*)tmp, n, 0, out);
+        hipStreamEndCapture(s, &g);
+        hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+        hipGraphLaunch(ge, s);  // in bounds: tmp is live
+        hipFree(tmp);
+        hipGraphLaunch(ge, s);  // tmp was freed
     } else {
         hipLaunchKernelGGL(read_kernel, dim3(1), dim3(64), 0, nullptr, x, n, strcmp(what, "oob") ? 0 : 1, out);
     }

@@ -5,8 +5,10 @@ against an emulated HIP device (one fiber per work-item, cross-lane
 operations as wavefront collectives) with AddressSanitizer, and driven
 through the C ABI by tests/emu/emu_model.cpp.  These tests check, without a
 GPU:
-  * that the emulator itself catches an out-of-bounds read and a cross-lane
-    operation reached by only part of a wavefront;
+  * that the emulator itself catches an out-of-bounds read, a cross-lane
+    operation reached by only part of a wavefront, and a host or freed
+    pointer handed to a kernel (device memory is host memory here, so every
+    kernel argument is checked against the live device allocations);
   * that whole teacher-forced model runs (prefill, then the captured
     one-kernel-per-op decode step) make no out-of-bounds access, in every
     weight type and activation mode, including the f32-activation kernels
@@ -82,6 +84,17 @@ def test_emulator_catches_out_of_bounds_and_divergence(emu):
     assert oob.returncode != 0 and "heap-buffer-overflow" in oob.stderr
     div = subprocess.run([st, "diverge"], capture_output=True, text=True, env=ENV)
     assert div.returncode != 0 and "cross-lane" in div.stderr
+
+
+@pytest.mark.parametrize("case,where", [("host", "stack"), ("hoststruct", "stack"), ("freed", "heap")])
+def test_emulator_refuses_host_and_freed_pointers(emu, case, where):
+    """Device memory is host memory in the emulator, so a host pointer or a
+    pointer into a freed allocation handed to a kernel would simply work
+    there.  Every argument word of every launch (and of every graph replay)
+    is checked against the live device allocations instead."""
+    p = subprocess.run([build_emu.SELFTEST, case], capture_output=True, text=True, env=ENV)
+    assert p.returncode != 0, p.stdout + p.stderr
+    assert "outside every live device allocation" in p.stderr and f"({where})" in p.stderr, p.stderr
 
 
 @pytest.mark.parametrize("wtype,mode,flags,bar", [
