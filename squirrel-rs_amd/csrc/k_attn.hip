@@ -173,8 +173,7 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
 }
 
-// Three workgroups per CU: the registers of the next K/V tile's loads fit
-// there without spilling (at four, 128 registers, they spill).
+// Three workgroups per CU (122 registers; four per CU measured the same).
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __restrict__ q,
                                                             const float* __restrict__ kc,
                                                             const float* __restrict__ vc, int pos0,
@@ -202,7 +201,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
     const int kv_dim = n_kv_heads * HD;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lk = lane >> 4;
-    const float scale = 1.0f / sqrtf((float)HD);
+    // Scores in base-2 units, s' = (q . k) * scale * log2(e), so that each
+    // probability is one exp2 (v_exp_f32): exp(x - m) = exp2(x' - m').
+    const float scale2 = (1.0f / sqrtf((float)HD)) * 1.44269504088896341f;
 
     // this lane's query (t0 + 16 wave + li) and its dims 16 lk .. 16 lk + 15
     const int tq = t0 + 16 * wave + li;
@@ -213,8 +214,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
         if (tq < m_rows) v = *(const float4*)(q + (size_t)tq * q_dim + h * HD + 16 * lk + 4 * c);
         qa[4 * c] = v.x; qa[4 * c + 1] = v.y; qa[4 * c + 2] = v.z; qa[4 * c + 3] = v.w;
     }
-    // online softmax state of query tq; o[dt][r] is O^T[16 dt + 4 lk + r][tq]
-    float mrow = -INFINITY, lrow = 0.0f;
+    // online softmax state of query tq: the running maximum (the same in
+    // its four lanes), this lane's part of the running sum, and
+    // o[dt][r] = O^T[16 dt + 4 lk + r][tq]
+    float mrow = -INFINITY, lpart = 0.0f;
     am_v4f o[4];
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) o[dt] = am_v4f{0.f, 0.f, 0.f, 0.f};
@@ -222,30 +225,32 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
     const int last_q = min(t0 + PT, m_rows) - 1;
     const int n_keys = pos0 + last_q + 1;  // keys any row of this tile can see
     const int limit = pos0 + tq;           // query tq sees keys 0 ..= limit
+    // Tiles below pos0 + t0 + 1 keys are visible to every query of the tile
+    // and need no mask.  A tile that reaches past n_keys is always a masked
+    // one, and key 0 is visible to every query, so each query's running
+    // maximum is finite from the first tile on.
+    const int unmasked_end = pos0 + t0 + 1;
 
     // This thread's four 16-byte units of a K tile (row e / 16, dims
     // 4 (e % 16) ..) and of a V tile (row e % 64, dims 4 (e / 64) ..) for
-    // e = tid + 256 i; rows past the last key read the last key and are
-    // zeroed.  A tile's loads are issued half an iteration before it is
-    // staged (K during the softmax and P.V, V during the next scores), so
-    // their latency is spent on work.
+    // e = tid + 256 i.  Rows past the last key read the last key (finite
+    // values): their scores are masked, and their probabilities are zero.
+    // A tile's loads are issued half an iteration before it is staged (K
+    // during the softmax and P.V, V during the next scores), so their
+    // latency is spent on work.
     float4 kreg[4], vreg[4];
     auto load_k = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
-            const bool ok = kb + r < n_keys;
-            const float4 v = *(const float4*)(kc + (size_t)(ok ? kb + r : n_keys - 1) * kv_dim + g * HD + 4 * c4);
-            kreg[i] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+            kreg[i] = *(const float4*)(kc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
         }
     };
     auto load_v = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e & 63, c4 = e >> 6;
-            const bool ok = kb + r < n_keys;
-            const float4 v = *(const float4*)(vc + (size_t)(ok ? kb + r : n_keys - 1) * kv_dim + g * HD + 4 * c4);
-            vreg[i] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+            vreg[i] = *(const float4*)(vc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
         }
     };
     auto store_k = [&]() {
@@ -292,33 +297,44 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
         // barrier that ended it); then the next tile's K rows are requested
         store_v();
         if (more) load_k(k0 + PT);
-        // scale, causal mask, online softmax (the four lanes of query tq
-        // hold its 64 scores)
+        // scale, causal mask (the tile's last keys only), online softmax
+        // (the four lanes of query tq hold its 64 scores)
         float tmax = -INFINITY;
+        if (k0 + PT > unmasked_end) {
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int kk = k0 + 16 * t + 4 * lk + r;
-                sc[t][r] = (kk <= limit && tq < m_rows) ? sc[t][r] * scale : -INFINITY;
-                tmax = fmaxf(tmax, sc[t][r]);
-            }
+                for (int r = 0; r < 4; r++) {
+                    const int kk = k0 + 16 * t + 4 * lk + r;
+                    sc[t][r] = kk <= limit ? sc[t][r] * scale2 : -INFINITY;
+                    tmax = fmaxf(tmax, sc[t][r]);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    sc[t][r] *= scale2;
+                    tmax = fmaxf(tmax, sc[t][r]);
+                }
+        }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        // finite (see unmasked_end); exp2(-inf) = 0 covers the first tile's
+        // alpha and the masked scores
         const float mn = fmaxf(mrow, tmax);
-        const float alpha = (mrow == -INFINITY) ? 0.0f : expf(mrow - mn);
+        const float alpha = __builtin_amdgcn_exp2f(mrow - mn);
         float rsum = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float p = (sc[t][r] == -INFINITY) ? 0.0f : expf(sc[t][r] - mn);
+                const float p = __builtin_amdgcn_exp2f(sc[t][r] - mn);
                 sc[t][r] = p;
                 rsum += p;
             }
-        rsum += __shfl_xor(rsum, 16, 64);
-        rsum += __shfl_xor(rsum, 32, 64);
-        lrow = lrow * alpha + rsum;
+        // the row sum stays split over the four lanes until the end
+        lpart = lpart * alpha + rsum;
         mrow = mn;
         __syncthreads();  // V staged; every wavefront is done with s_k
         // O^T[dt] = alpha O^T[dt] + V^T[16 dt + li][keys] P^T[keys][tq] over the 64 keys
@@ -340,6 +356,8 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
         }
         __syncthreads();  // the next K staged; every wavefront is done with s_vt
     }
+    float lrow = lpart + __shfl_xor(lpart, 16, 64);
+    lrow += __shfl_xor(lrow, 32, 64);
     if (tq < m_rows) {
         const float inv = 1.0f / lrow;
 #pragma unroll
