@@ -173,7 +173,8 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
 }
 
-// Three workgroups per CU (122 registers; four per CU measured the same).
+// Three workgroups per CU (152 registers; capped at 128 for four per CU,
+// 11 of them spill, and it measured the same).
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __restrict__ q,
                                                             const float* __restrict__ kc,
                                                             const float* __restrict__ vc, int pos0,
@@ -237,37 +238,39 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
     // values): their scores are masked, and their probabilities are zero.
     // A tile's loads are issued half an iteration before it is staged (K
     // during the softmax and P.V, V during the next scores), so their
-    // latency is spent on work.
-    float4 kreg[4], vreg[4];
+    // latency is spent on work.  The registers are vector-typed: with float4
+    // (a struct) the copies global -> registers -> LDS were kept in scratch
+    // memory (10% of the kernel's time).
+    am_v4f kreg[4], vreg[4];
     auto load_k = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
-            kreg[i] = *(const float4*)(kc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
+            kreg[i] = *(const am_v4f*)(kc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
         }
     };
     auto load_v = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e & 63, c4 = e >> 6;
-            vreg[i] = *(const float4*)(vc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
+            vreg[i] = *(const am_v4f*)(vc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
         }
     };
     auto store_k = [&]() {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
-            *(float4*)&s_k[r][4 * c4] = kreg[i];
+            *(am_v4f*)&s_k[r][4 * c4] = kreg[i];
         }
     };
     auto store_v = [&]() {  // transposed
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e & 63, c4 = e >> 6;
-            s_vt[4 * c4][r] = vreg[i].x;
-            s_vt[4 * c4 + 1][r] = vreg[i].y;
-            s_vt[4 * c4 + 2][r] = vreg[i].z;
-            s_vt[4 * c4 + 3][r] = vreg[i].w;
+            s_vt[4 * c4][r] = vreg[i][0];
+            s_vt[4 * c4 + 1][r] = vreg[i][1];
+            s_vt[4 * c4 + 2][r] = vreg[i][2];
+            s_vt[4 * c4 + 3][r] = vreg[i][3];
         }
     };
     load_k(0);
