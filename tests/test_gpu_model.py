@@ -54,6 +54,13 @@ def run_oracle(path, seq, mode, max_pos=256):
     return outs
 
 
+def forward_steps(seq):
+    """The forward calls of a teacher-forced sequence: the prompt, then one
+    token per call; an entry that is already a list or array (a chunk of
+    several tokens) is one call of its own."""
+    return [seq[0]] + [t if isinstance(t, (list, np.ndarray)) else [t] for t in seq[1:]]
+
+
 def run_gpu(path, seq, f32_acts=False, graph=True, max_pos=256, persistent=True, taps=True):
     """Teacher-forced device run: logits, device argmax and (integer path)
     the Q8_0 blocks of every quantization site of every step."""
@@ -63,7 +70,7 @@ def run_gpu(path, seq, f32_acts=False, graph=True, max_pos=256, persistent=True,
     if taps:
         c.act_taps(True)
     outs, toks, blocks = [], [], []
-    for ids in [seq[0]] + [[t] for t in seq[1:]]:
+    for ids in forward_steps(seq):
         c.forward(ids)
         outs.append(c.logits())
         toks.append(c.argmax())
@@ -87,7 +94,7 @@ def check_logits(path, seq, got, blocks, label, max_pos=256):
     om = O.OracleModel(path)
     oc = om.new_context(max_pos, O.W8A8)
     rows = []
-    for step, (ids, g, blk) in enumerate(zip([seq[0]] + [[t] for t in seq[1:]], got, blocks)):
+    for step, (ids, g, blk) in enumerate(zip(forward_steps(seq), got, blocks)):
         st = oc.forward(ids, lock=blk, tol=LOCK_TOL)
         w = oc.logits()
         rows.append((step, rel_l2(g, w), float(np.abs(g - w).max()), st))
@@ -116,6 +123,24 @@ def test_teacher_forced_logits(tiny_gguf, wtype, variant, decode):
     check_logits(path, seq, got, blocks, f"{wtype}/{variant}/{decode}")
     for g, t in zip(got, toks):
         assert t == O.greedy(g), "device argmax disagrees with the greedy rule on its own logits"
+
+
+@pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
+def test_prefill_continues_after_earlier_positions(tiny_gguf, wtype):
+    """A multi-token forward at a later position (model.rs:45-97 with the
+    context already holding tokens): a 40-token prompt, then a 90-token chunk
+    at positions 40..129 (its two 64-row query tiles see 40 earlier keys and
+    a partial last key tile), then decode steps, phase-locked to the oracle
+    doing the same calls."""
+    path = tiny_gguf(wtype, "g4")
+    vocab = O.OracleModel(path).cfg.vocab
+    r = np.random.default_rng(29)
+    seq = [r.integers(0, vocab, 40).astype(np.uint32), r.integers(0, vocab, 90).astype(np.uint32)]
+    seq += [int(t) for t in r.integers(0, vocab, 4)]
+    got, toks, (m, c, blocks) = run_gpu(path, seq)
+    check_logits(path, seq, got, blocks, f"{wtype}/chunked")
+    for g, t in zip(got, toks):
+        assert t == O.greedy(g)
 
 
 @pytest.mark.skip(reason=A32_SKIP)
@@ -268,7 +293,7 @@ def test_step_instances_agree(tiny_gguf, wtype):
     assert c.persistent
     c.step_trace(True)
     traced = []
-    for ids in [seq[0]] + [[t] for t in seq[1:]]:
+    for ids in forward_steps(seq):
         c.forward(ids)
         traced.append(c.logits())
     assert lean_toks == tapped_toks
