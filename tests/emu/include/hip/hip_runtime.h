@@ -307,6 +307,8 @@ inline sqemu_v16f mfma_f32_32x32x8f16(sqemu_v4h a, sqemu_v4h b, sqemu_v16f c) {
 #define __builtin_amdgcn_wave_barrier() ::sqemu::wave_barrier()
 #define __builtin_amdgcn_update_dpp(o, s, c, r, b, bc) ::sqemu::update_dpp((o), (s), (c), (r), (b), (bc))
 #define __builtin_amdgcn_readlane(v, l) ::sqemu::readlane((v), (l))
+// scheduling hints have no effect on the emulated execution
+#define __builtin_amdgcn_sched_barrier(m) ((void)(m))
 // v_exp_f32 (2^x): the host exp2f stands in for the device instruction
 #define __builtin_amdgcn_exp2f(x) ::exp2f((float)(x))
 #define __builtin_amdgcn_sdot4(a, b, c, cl) ::sqemu::sdot4((a), (b), (c), (cl))
