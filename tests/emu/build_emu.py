@@ -57,8 +57,10 @@ def sources(asan: bool):
             dst = os.path.join(BUILD, "src", f.rsplit(".", 1)[0] + ".cpp")
             new = rewrite(open(p).read())
             if not os.path.exists(dst) or open(dst).read() != new:
-                with open(dst, "w") as fh:
+                tmp = f"{dst}.{os.getpid()}.tmp"
+                with open(tmp, "w") as fh:
                     fh.write(new)
+                os.replace(tmp, dst)
             jobs.append(dst)
     jobs += [os.path.join(HERE, "emu.cpp"), os.path.join(HERE, "step_stub.cpp"),
              os.path.join(HERE, "emu_model.cpp"), os.path.join(HERE, "selftest.cpp")]
@@ -84,7 +86,13 @@ def compile_one(src: str, asan: bool):
                                       if h.endswith(".h")),
             os.path.getmtime(os.path.join(HERE, "include", "hip", "hip_runtime.h"))):
         return obj, "", 0
+    # written under a private name and renamed, so that concurrent builds
+    # (parallel test workers) never see a partial object
+    tmp = f"{obj}.{os.getpid()}.tmp"
+    cmd[-1] = tmp
     p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode == 0:
+        os.replace(tmp, obj)
     return obj, p.stdout + p.stderr, p.returncode
 
 
@@ -102,11 +110,13 @@ def build(asan: bool = True) -> str:
     drv = [o for o in objs if os.path.basename(o).startswith("emu_model")]
     st = [o for o in objs if os.path.basename(o).startswith("selftest")]
     for exe, parts in ((EXE, emu + lib + drv), (SELFTEST, emu + st)):
-        cmd = [CLANG, *flags(asan), *parts, "-o", exe, "-lm", "-lpthread"]
+        tmp = f"{exe}.{os.getpid()}.tmp"
+        cmd = [CLANG, *flags(asan), *parts, "-o", tmp, "-lm", "-lpthread"]
         p = subprocess.run(cmd, capture_output=True, text=True)
         if p.returncode:
             print(p.stdout + p.stderr, file=sys.stderr)
             raise RuntimeError("link failed")
+        os.replace(tmp, exe)
     return EXE
 
 
