@@ -217,12 +217,13 @@ int sq_quantize_row_q8_0(const float* d_x, size_t n, void* d_blocks);
 int sq_linear(const float* d_in, size_t m, size_t k, const sq_weight* w, float* d_out,
               uint32_t flags);
 /* No counterpart in the reference: sq_linear for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
- * sq_linear, but the scratch (Q8_0 activations and K-split partial tiles)
- * is a static per-GPU device array of 20.25 MiB: m * k may not exceed
- * 4 Mi elements (SQ_ERR_SHAPE otherwise).  Calls that overlap on one GPU
- * share that array and race; each call is synchronous. */
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as sq_linear, but the
+ * scratch (Q8_0 activations and K-split partial tiles) is a static per-GPU
+ * device array of 20.25 MiB: m * k may not exceed 4 Mi elements
+ * (SQ_ERR_SHAPE otherwise).  Calls that overlap on one GPU share that array
+ * and race.  Each call runs on the null stream and synchronizes it, so it
+ * cannot be recorded under a stream capture. */
 int sq_linear_noalloc(const float* d_in, size_t m, size_t k, const sq_weight* w, float* d_out,
                       uint32_t flags);
 /* linear_shared (src/ops/linear.rs:73-168): several projections of one input,

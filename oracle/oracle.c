@@ -755,8 +755,31 @@ const float* or_ctx_last_hidden(const or_ctx* c) { return c->last_hidden; }
 /* Phase lock (see oracle.h): compare the device's blocks of one site with
  * the oracle's own, count, and continue with the device's. */
 static void lock_site(or_lock* lk, const float* x, size_t rows, size_t k, or_block_q8_0* own,
-                      const or_block_q8_0* dev, int layer, int site) {
+                      const or_block_q8_0* dev_in, int layer, int site) {
     size_t nb = rows * k / 32;
+    or_block_q8_0* planted = NULL;
+    const or_block_q8_0* dev = dev_in;
+    if (lk->plant_quanta != 0.0f && layer == lk->plant_layer && site == lk->plant_site) {
+        /* the planted error: this site's blocks as an implementation whose
+         * scaled values are all off by plant_quanta would produce them */
+        planted = (or_block_q8_0*)malloc(nb * sizeof(or_block_q8_0));
+        for (size_t b = 0; b < nb; b++) {
+            const float* xb = x + b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(xb[i]));
+            float scale = amax / 127.0f;
+            float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            planted[b].d = own[b].d;
+            for (int i = 0; i < 32; i++) {
+                float v = roundf(xb[i] * inv + lk->plant_quanta);
+                v = fminf(127.0f, fmaxf(-127.0f, v));
+                planted[b].qs[i] = isnan(v) ? (int8_t)0 : (int8_t)v;
+            }
+        }
+        dev = planted;
+    }
+    const int kind = site < 5 ? site : 4;
+    lk->site_values[kind] += nb * 32;
     for (size_t b = 0; b < nb; b++) {
         const float* xb = x + b * 32;
         lk->values += 32;
@@ -774,21 +797,26 @@ static void lock_site(or_lock* lk, const float* x, size_t rows, size_t k, or_blo
             int adjacent = ((own[b].d ^ dev[b].d) & 0x8000) == 0 &&
                            (own[b].d > dev[b].d ? own[b].d - dev[b].d : dev[b].d - own[b].d) == 1;
             float mid = 0.5f * (or_f16_to_f32(own[b].d) + or_f16_to_f32(dev[b].d));
-            if (!adjacent || fabsf(scale - mid) > 1e-5f * fabsf(mid)) {
+            float rel = fabsf(scale - mid) / fabsf(mid);
+            if (!adjacent || !(rel <= 1e-5f)) {
                 ok = 0;
                 bad_i = b * 32;
                 bad_dist = -1.0f;
             } else {
                 lk->scale_flips++;
+                if (rel > lk->max_scale_rel) lk->max_scale_rel = rel;
             }
         }
+        uint64_t flips = 0;
+        float maxd = 0.0f;
         for (int i = 0; i < 32 && ok; i++) {
             int qo = own[b].qs[i], qd = dev[b].qs[i];
             if (qo == qd) continue;
             float v = fabsf(xb[i] * inv);
             float dist = fabsf((v - floorf(v)) - 0.5f);
             if ((qo - qd == 1 || qd - qo == 1) && dist <= lk->tol) {
-                lk->flips++;
+                flips++;
+                if (dist > maxd) maxd = dist;
             } else {
                 ok = 0;
                 bad_i = b * 32 + (size_t)i;
@@ -803,9 +831,14 @@ static void lock_site(or_lock* lk, const float* x, size_t rows, size_t k, or_blo
                 lk->first_bad_dist = bad_dist;
             }
             lk->bad++;
+        } else {
+            lk->flips += flips;
+            lk->site_flips[kind] += flips;
+            if (maxd > lk->max_flip_dist) lk->max_flip_dist = maxd;
         }
         own[b] = dev[b];
     }
+    free(planted);
 }
 
 /* The quantized activations of one site: the oracle's own, or under a lock
@@ -893,7 +926,7 @@ int or_forward_locked(const or_llama* m, or_ctx* c, const uint32_t* ids, size_t 
      * (model.rs:72-95). */
     or_rms_norm_rows(c->hidden + (n - 1) * D, m->output_norm, c->last_hidden, 1, D, m->eps);
     if (int_acts) {
-        const or_block_q8_0* a = site_blocks(c, c->last_hidden, 1, D, lock, &dev, m->n_layers, 0);
+        const or_block_q8_0* a = site_blocks(c, c->last_hidden, 1, D, lock, &dev, m->n_layers, 4);
         return or_linear_prequant(a, 1, D, wt, m->output, (size_t)m->vocab, c->logits, mode);
     }
     return or_linear(c->last_hidden, 1, D, wt, m->output, (size_t)m->vocab, c->logits, mode);

@@ -144,7 +144,9 @@ int or_linear_prequant(const or_block_q8_0* aq, size_t m, size_t k, int wtype, c
  * block scale may differ by one binary16 step only where the f32 scale lies
  * at the midpoint of the two.  Everything else counts as bad.  The forward
  * then continues with the implementation's blocks, so the logits compare the
- * two at f32 rounding level.  Integer modes only. */
+ * two at f32 rounding level.  Integer modes only.  Sites are numbered 0
+ * attention-norm output, 1 attention output, 2 FFN-norm output, 3 FFN
+ * activation (layers 0..n-1), and 4 the LM-head input (layer n). */
 typedef struct {
     const or_block_q8_0* blocks;
     float tol;
@@ -152,6 +154,18 @@ typedef struct {
     int first_bad_layer, first_bad_site;
     size_t first_bad_index;
     float first_bad_dist; /* distance from the midpoint, -1 for a scale mismatch */
+    /* the largest distance from a midpoint (quanta) of an accepted element
+     * flip, and the largest |scale - midpoint| / midpoint of an accepted
+     * scale flip */
+    float max_flip_dist;
+    float max_scale_rel;
+    uint64_t site_values[5], site_flips[5];
+    /* Test hook, a planted systematic error: when plant_quanta is non-zero,
+     * the implementation's blocks of site (plant_layer, plant_site) are
+     * replaced, before the check, by the oracle's own quantization of that
+     * site with every scaled value moved by plant_quanta quanta. */
+    int plant_layer, plant_site;
+    float plant_quanta;
 } or_lock;
 int or_forward_locked(const or_llama* m, or_ctx* c, const uint32_t* ids, size_t n, or_lock* lock);
 

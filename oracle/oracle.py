@@ -321,7 +321,10 @@ class OrLock(C.Structure):
     _fields_ = [("blocks", C.c_void_p), ("tol", C.c_float), ("values", C.c_uint64),
                 ("flips", C.c_uint64), ("scale_flips", C.c_uint64), ("bad", C.c_uint64),
                 ("first_bad_layer", C.c_int), ("first_bad_site", C.c_int),
-                ("first_bad_index", C.c_size_t), ("first_bad_dist", C.c_float)]
+                ("first_bad_index", C.c_size_t), ("first_bad_dist", C.c_float),
+                ("max_flip_dist", C.c_float), ("max_scale_rel", C.c_float),
+                ("site_values", C.c_uint64 * 5), ("site_flips", C.c_uint64 * 5),
+                ("plant_layer", C.c_int), ("plant_site", C.c_int), ("plant_quanta", C.c_float)]
 
 
 class OracleModel:
@@ -368,11 +371,14 @@ class OracleContext:
         self.m = model
         self.h = lib().or_ctx_new(C.byref(model.s), max_positions, mode)
 
-    def forward(self, ids, lock=None, tol: float = 0.02):
+    def forward(self, ids, lock=None, tol: float = 0.02, plant=None):
         """One Llama3_2::forward.  With `lock` (an implementation's Q8_0
         blocks of every quantization site, oracle.h or_lock order) the
         integer path checks each site against its own quantization and then
-        continues with the given blocks; returns the lock's counts."""
+        continues with the given blocks; returns the lock's counts.  `plant`
+        = (layer, site, quanta) replaces that site's given blocks by the
+        oracle's own quantization with every scaled value moved by `quanta`
+        (a planted systematic error, for tests of the lock)."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         if lock is None:
             st = lib().or_forward(C.byref(self.m.s), self.h, _p(ids), ids.size)
@@ -386,12 +392,16 @@ class OracleContext:
         if blocks.dtype != BLOCK_Q8_0 or blocks.size != need:
             raise ValueError(f"lock needs {need} Q8_0 blocks, got {blocks.size}")
         lk = OrLock(blocks.ctypes.data, tol)
+        if plant is not None:
+            lk.plant_layer, lk.plant_site, lk.plant_quanta = int(plant[0]), int(plant[1]), float(plant[2])
         st = lib().or_forward_locked(C.byref(self.m.s), self.h, _p(ids), ids.size, C.byref(lk))
         if st:
             raise RuntimeError(f"oracle forward status {st}")
         return {"values": lk.values, "flips": lk.flips, "scale_flips": lk.scale_flips, "bad": lk.bad,
                 "first_bad": (lk.first_bad_layer, lk.first_bad_site, lk.first_bad_index, lk.first_bad_dist)
-                if lk.bad else None}
+                if lk.bad else None,
+                "max_flip_dist": float(lk.max_flip_dist), "max_scale_rel": float(lk.max_scale_rel),
+                "site_values": list(lk.site_values), "site_flips": list(lk.site_flips)}
 
     def logits(self) -> np.ndarray:
         p = lib().or_ctx_logits(self.h)

@@ -145,21 +145,7 @@ void sq_ctx_free(sq_ctx* c) { ctx_destroy(c); }
 
 int sq_ctx_reset(sq_ctx* c) {
     if (!c) return set_error(SQ_ERR_ARG, "reset: null context");
-    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
-    c->seq_len = 0;
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
-    if (c->persist) {
-        // Clear a raised error and move the tag epoch past every tag an
-        // abandoned step may have written (tags are never reused).
-        unsigned epoch = 0;
-        SQ_HIP_CHECK(hipMemcpy(&epoch, c->s_epoch, 4, hipMemcpyDeviceToHost));
-        epoch += 2u * (6u * (unsigned)c->m->cfg.n_layers + 2u);
-        SQ_HIP_CHECK(hipMemcpy(c->s_epoch, &epoch, 4, hipMemcpyHostToDevice));
-        SQ_HIP_CHECK(hipMemset(c->s_error, 0, 4));
-    }
-    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
-    return 0;
+    return ctx_reset(c);
 }
 
 int sq_ctx_decode_kernel(const sq_ctx* c) { return c && c->persist ? 1 : 0; }
@@ -413,7 +399,17 @@ int sq_embed(const uint32_t* d_tokens, size_t n, const sq_weight* table, float* 
     if (!table) return set_error(SQ_ERR_ARG, "embed: null table");
     if (table->m.wtype == WT_BF16) return set_error(SQ_ERR_UNSUPPORTED, kA32Disabled);
     if (n == 0) return 0;
-    return finish(launch_embed(nullptr, view(table->m), table->m.wtype, d_tokens, (int)n, table->m.k, d_out));
+    Tmp err;
+    int st;
+    if ((st = err.alloc(4))) return st;
+    SQ_HIP_CHECK(hipMemsetAsync(err.p, 0, 4, nullptr));
+    if ((st = finish(launch_embed(nullptr, view(table->m), table->m.wtype, d_tokens, (int)n, table->m.k, d_out,
+                                  (uint32_t*)err.p))))
+        return st;
+    uint32_t bad = 0;
+    SQ_HIP_CHECK(hipMemcpy(&bad, err.p, 4, hipMemcpyDeviceToHost));
+    if (bad) return set_error(SQ_ERR_ARG, "embed: a token id is past the embedding table (embedding.rs:43-44)");
+    return 0;
 }
 
 int sq_rms_norm(const float* d_in, const float* d_w, float* d_out, size_t rows, size_t dim, float eps) {
@@ -497,11 +493,14 @@ int sq_log_softmax_at(const float* d_logits, size_t n, uint32_t idx, double* out
     if (n == 0) return set_error(SQ_ERR_EMPTY, "log_softmax_at: EmptyInput");
     if (idx >= n) return set_error(SQ_ERR_ARG, "log_softmax_at: index out of range");
     if (n > (size_t)INT32_MAX) return set_error(SQ_ERR_SHAPE, "log_softmax_at: row too long");
-    Tmp id, val;
+    Tmp id, val, err;
     int st;
-    if ((st = id.alloc(4)) || (st = val.alloc(8))) return st;
+    if ((st = id.alloc(4)) || (st = val.alloc(8)) || (st = err.alloc(4))) return st;
     SQ_HIP_CHECK(hipMemcpy(id.p, &idx, 4, hipMemcpyHostToDevice));
-    if ((st = launch_log_softmax_at(nullptr, d_logits, (int)n, (const uint32_t*)id.p, (double*)val.p))) return st;
+    SQ_HIP_CHECK(hipMemsetAsync(err.p, 0, 4, nullptr));
+    if ((st = launch_log_softmax_at(nullptr, d_logits, (int)n, (const uint32_t*)id.p, (double*)val.p,
+                                    (uint32_t*)err.p)))
+        return st;
     if ((st = finish(0))) return st;
     SQ_HIP_CHECK(hipMemcpy(out, val.p, 8, hipMemcpyDeviceToHost));
     return 0;

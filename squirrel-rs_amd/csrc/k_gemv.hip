@@ -153,7 +153,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     int ASUM[NBL];
     if constexpr (PRO == PRO_NORM) {
         const bool from_embed = a.embd.qs != nullptr;
-        const uint32_t tok = from_embed ? min(*a.token, (uint32_t)(a.embd.rows - 1)) : 0u;
+        // an id past the table is the reference's panic (embedding.rs:43-44):
+        // the read is clamped in bounds and the error word tells the host
+        const uint32_t tok_in = from_embed ? *a.token : 0u;
+        const uint32_t tok = min(tok_in, (uint32_t)(a.embd.rows - 1));
+        if (tok_in != tok && t == 0 && tid == 0) *a.id_error = 1u;
 #pragma unroll
         for (int j = 0; j < G::EPT; j++) {
             const int i = tid + j * G::NT;
@@ -540,8 +544,9 @@ int launch_gemv(hipStream_t s, int pro, int epi, bool a8, const GemvArgs& a, int
         return set_error(SQ_ERR_SHAPE, "gemv: k must be a positive multiple of 32");
     if (epi == EPI_GATEUP && a.n_rows % 32 != 0)
         return set_error(SQ_ERR_SHAPE, "gemv: gate/up width must be a multiple of 32");
-    if (a.embd.qs != nullptr && (a.token == nullptr || a.hidden_out == nullptr || a.embd.k != a.w.k))
-        return set_error(SQ_ERR_ARG, "gemv: embedding prologue needs a token, a hidden output and k = dim");
+    if (a.embd.qs != nullptr &&
+        (a.token == nullptr || a.id_error == nullptr || a.hidden_out == nullptr || a.embd.k != a.w.k))
+        return set_error(SQ_ERR_ARG, "gemv: embedding prologue needs a token, an error word, a hidden output and k = dim");
     switch (a.w.wtype) {
         case WT_Q8_0:
             return a8 ? dispatch<WT_Q8_0, true>(s, pro, epi, a, grid_out)

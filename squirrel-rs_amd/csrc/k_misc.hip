@@ -20,12 +20,17 @@ inline int check_launch(const char* what) {
 // embed_blocks (src/ops/embedding.rs:23-52) with dequantize_into
 // (src/kernels/dot_prod.rs:409-414, 440-446, 524-528): exact.
 __global__ __launch_bounds__(kBlock) void embed_kernel(MatView table, const uint32_t* tokens,
-                                                        int dim, float* out) {
+                                                        int dim, float* out, uint32_t* id_error) {
     const int t = blockIdx.x;
     uint32_t tok = tokens[t];
-    // ids are validated on the host; the unsigned compare also catches
-    // values of 2^31 and more, which a signed one would let through
-    if (tok >= (uint32_t)table.rows) tok = table.rows - 1;
+    // The reference indexes the table with the id and panics past its end
+    // (embedding.rs:43-44).  Here the row read stays in bounds (an unsigned
+    // compare, so ids of 2^31 and more are caught too) and the error word
+    // tells the host, which turns it into a status.
+    if (tok >= (uint32_t)table.rows) {
+        if (threadIdx.x == 0) *id_error = 1u;
+        tok = table.rows - 1;
+    }
     const int KB = dim >> 5;
     float* o = out + (size_t)t * dim;
     for (int e = threadIdx.x; e < dim; e += kBlock) {
@@ -463,7 +468,8 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const float* logits,
 // so the two agree to f64 rounding.
 __global__ __launch_bounds__(1024) void log_softmax_at_kernel(const float* __restrict__ logits, int n,
                                                               const uint32_t* __restrict__ idx,
-                                                              double* __restrict__ out) {
+                                                              double* __restrict__ out,
+                                                              uint32_t* __restrict__ id_error) {
     __shared__ float s_m[16];
     __shared__ double s_s[16];
     const int tid = threadIdx.x;
@@ -483,7 +489,10 @@ __global__ __launch_bounds__(1024) void log_softmax_at_kernel(const float* __res
     if (tid == 0) {
         double tot = 0.0;
         for (int w = 0; w < 16; w++) tot += s_s[w];
-        *out = (double)logits[*idx] - md - log(tot);
+        // an index past the row is the reference's panic (perplexity.rs:112-117)
+        const uint32_t i = *idx;
+        if (i >= (uint32_t)n) *id_error = 1u;
+        *out = i < (uint32_t)n ? (double)logits[i] - md - log(tot) : (double)NAN;
     }
 }
 
@@ -517,10 +526,11 @@ __global__ void copy_i32_kernel(const int* src, int* dst) { *dst = *src; }
 }  // namespace
 
 int launch_embed(hipStream_t s, const MatView& table, int wtype, const uint32_t* tokens, int n_tokens,
-                 int dim, float* out) {
+                 int dim, float* out, uint32_t* id_error) {
+    if (!id_error) return set_error(SQ_ERR_ARG, "embed: no error word");
     MatView t = table;
     t.wtype = wtype;
-    hipLaunchKernelGGL(embed_kernel, dim3(n_tokens), dim3(kBlock), 0, s, t, tokens, dim, out);
+    hipLaunchKernelGGL(embed_kernel, dim3(n_tokens), dim3(kBlock), 0, s, t, tokens, dim, out, id_error);
     return check_launch("embed");
 }
 
@@ -621,8 +631,10 @@ int launch_block_isums(hipStream_t s, const int8_t* aq, const MatView& w, int wt
     return check_launch("block_isums");
 }
 
-int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint32_t* idx, double* out) {
-    hipLaunchKernelGGL(log_softmax_at_kernel, dim3(1), dim3(1024), 0, s, logits, n, idx, out);
+int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint32_t* idx, double* out,
+                          uint32_t* id_error) {
+    if (!id_error) return set_error(SQ_ERR_ARG, "log_softmax_at: no error word");
+    hipLaunchKernelGGL(log_softmax_at_kernel, dim3(1), dim3(1024), 0, s, logits, n, idx, out, id_error);
     return check_launch("log_softmax_at");
 }
 

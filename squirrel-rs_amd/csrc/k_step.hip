@@ -861,7 +861,11 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     auto tag = [&](int l, int ph) -> unsigned { return epoch + 1u + (unsigned)(l * PH_PER_LAYER + ph); };
     const unsigned head_tag = epoch + 1u + (unsigned)(a.n_layers * PH_PER_LAYER);
     const int pos = *a.pos;
-    const uint32_t tok = *a.token;
+    // an id past the table is the reference's panic (embedding.rs:43-44):
+    // the read is clamped in bounds and the error word tells the host
+    const uint32_t tok_in = *a.token;
+    const uint32_t tok = min(tok_in, (uint32_t)(a.embd.rows - 1));
+    if (tok_in != tok && blockIdx.x == 0 && threadIdx.x == 0) *a.id_error = 1u;
     const int P = pos + 1;
     const int ntiles = (P + TPOS - 1) / TPOS;
     // Attention work: chunks of tpc consecutive 64-position tiles per KV

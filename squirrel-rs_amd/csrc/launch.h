@@ -50,6 +50,7 @@ struct GemvArgs {
     // (when embd.qs is non-null); workgroup 0 also stores x to hidden_out.
     MatView embd;
     const uint32_t* token;
+    uint32_t* id_error;  // set when *token is past the table (the read is clamped)
     float* hidden_out;
     // taps of the prologue, written by workgroup 0 when non-null: the
     // normalized row (f32) and, on the integer path, its Q8_0 blocks
@@ -81,8 +82,9 @@ int launch_sdpa_generic(hipStream_t s, const float* q, const float* k, const flo
                         int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim);
 
 // ---- row kernels (k_misc.hip) -------------------------------------------
+// An id past the table sets *id_error (the row read is clamped in bounds).
 int launch_embed(hipStream_t s, const MatView& table, int wtype, const uint32_t* tokens,
-                 int n_tokens, int dim, float* out);
+                 int n_tokens, int dim, float* out, uint32_t* id_error);
 int launch_rmsnorm_rows(hipStream_t s, const float* x, const float* w, int rows, int dim,
                         float eps, float* out, int8_t* act_q, uint16_t* act_d);
 int launch_quantize_rows(hipStream_t s, const float* x, size_t n, int8_t* qs, uint16_t* d);
@@ -117,7 +119,8 @@ int launch_block_isums(hipStream_t s, const int8_t* aq, const MatView& w, int wt
                        int32_t* out);
 int launch_copy_i32(hipStream_t s, const int* src, int* dst);
 // out = log p(*idx) under softmax(logits[0..n)) in f64 (*idx < n).
-int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint32_t* idx, double* out);
+int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint32_t* idx, double* out,
+                          uint32_t* id_error);
 
 // ---- prefill matmul (k_gemm.hip) ----------------------------------------
 // out[m, rows] (+)= in[m, k] @ W.  a8: activations given as Q8_0 (aq/ad,
@@ -181,6 +184,7 @@ struct StepArgs {
     int max_tiles;
     unsigned* epoch;
     int* error;
+    uint32_t* id_error;  // set when *token is past the embedding table
     long long spin_limit;
     float* dbg_normed;  // layer-0 attention norm (workgroup 0), optional
     // Quantized activations of every site (the context's tap_q / tap_d

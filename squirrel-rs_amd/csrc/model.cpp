@@ -464,6 +464,7 @@ int build_decode_step(sq_ctx* c) {
             // embed (model.rs:57-62) fused into the first norm prologue
             q.embd = view(m->embd);
             q.token = c->d_token;
+            q.id_error = c->d_id_error;
             q.hidden_out = c->hidden;
             q.dbg_normed = c->dbg_normed;
         }
@@ -629,7 +630,7 @@ int run_prefill(sq_ctx* c, size_t n) {
     };
     if ((st = phase(2))) return st;
     SQ_HIP_CHECK(hipMemcpyAsync(c->d_ids, c->h_pinned, n * 4, hipMemcpyHostToDevice, s));
-    if ((st = launch_embed(s, view(m->embd), m->wtype, c->d_ids, (int)n, D, c->p_hidden))) return st;
+    if ((st = launch_embed(s, view(m->embd), m->wtype, c->d_ids, (int)n, D, c->p_hidden, c->d_id_error))) return st;
     const int pos0 = (int)c->seq_len;
     const int N = (int)n;
     const size_t kv_layer = c->max_pos * (size_t)KVD;
@@ -756,6 +757,7 @@ int setup_persistent(sq_ctx* c) {
     a.max_tiles = c->max_tiles;
     a.epoch = c->s_epoch;
     a.error = c->s_error;
+    a.id_error = c->d_id_error;
     a.spin_limit = (long long)khz * 250;  // 250 ms
     a.dbg_normed = c->dbg_normed;
     a.dbg_qs = c->tap_q;
@@ -777,12 +779,38 @@ int setup_persistent(sq_ctx* c) {
 }
 
 int ctx_check(sq_ctx* c) {
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    uint32_t id_err = 0;
+    SQ_HIP_CHECK(hipMemcpy(&id_err, c->d_id_error, 4, hipMemcpyDeviceToHost));
+    if (id_err)
+        return set_error(SQ_ERR_ARG, "forward: a token id on the device is past the embedding table "
+                                     "(embedding.rs:43-44); the context must be reset");
     if (!c->persist) return 0;
     int err = 0;
-    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
     SQ_HIP_CHECK(hipMemcpy(&err, c->s_error, 4, hipMemcpyDeviceToHost));
     if (err)
         return set_error(SQ_ERR_HIP, "decode step: a grid barrier wait timed out; the context must be reset");
+    return 0;
+}
+
+int ctx_reset(sq_ctx* c) {
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+    c->seq_len = 0;
+    // every write on the context's own stream, so the next launch there is
+    // ordered after them
+    SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
+    SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
+    SQ_HIP_CHECK(hipMemsetAsync(c->d_id_error, 0, 4, c->stream));
+    if (c->persist) {
+        unsigned epoch = 0;
+        SQ_HIP_CHECK(hipMemcpyAsync(&epoch, c->s_epoch, 4, hipMemcpyDeviceToHost, c->stream));
+        SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
+        epoch += 2u * (6u * (unsigned)c->m->cfg.n_layers + 2u);
+        c->h_pinned[0] = epoch;
+        SQ_HIP_CHECK(hipMemcpyAsync(c->s_epoch, c->h_pinned, 4, hipMemcpyHostToDevice, c->stream));
+        SQ_HIP_CHECK(hipMemsetAsync(c->s_error, 0, 4, c->stream));
+    }
+    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
     return 0;
 }
 
@@ -822,7 +850,7 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
         (st = dmalloc(&c->pi, c->n_parts)) || (st = dmalloc(&c->pn, c->n_parts)) ||
         (st = dmalloc(&c->dbg_normed, D)) || (st = dmalloc(&c->last_hidden, D)) || (st = dmalloc(&c->head_qs, D)) ||
         (st = dmalloc(&c->head_d, D / 32)) || (st = dmalloc(&c->d_sids, max_pos + 1)) ||
-        (st = dmalloc(&c->d_logp, max_pos + 1)))
+        (st = dmalloc(&c->d_logp, max_pos + 1)) || (st = dmalloc(&c->d_id_error, 1)))
         return fail(st);
     he = hipHostMalloc((void**)&c->h_pinned, (max_pos + 16) * sizeof(uint32_t), hipHostMallocDefault);
     if (he != hipSuccess) return fail(set_error(SQ_ERR_HIP, std::string("hipHostMalloc: ") + hipGetErrorString(he)));
@@ -846,6 +874,7 @@ int ctx_create(const sq_model* m, size_t max_pos, uint32_t flags, sq_ctx** out) 
     SQ_HIP_CHECK(hipMemset(c->d_pos, 0, 4));
     SQ_HIP_CHECK(hipMemset(c->d_nhist, 0, 4));
     SQ_HIP_CHECK(hipMemset(c->d_token, 0, 4));
+    SQ_HIP_CHECK(hipMemset(c->d_id_error, 0, 4));
     SQ_HIP_CHECK(hipMemset(c->kcache, 0, (size_t)g.n_layers * max_pos * KVD * 4));
     SQ_HIP_CHECK(hipMemset(c->vcache, 0, (size_t)g.n_layers * max_pos * KVD * 4));
 
@@ -880,7 +909,7 @@ void ctx_destroy(sq_ctx* c) {
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
     dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad); dfree(c->p_split);
     dfree(c->d_layers); dfree(c->s_stream); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
-    dfree(c->d_sids); dfree(c->d_logp);
+    dfree(c->d_sids); dfree(c->d_logp); dfree(c->d_id_error);
     if (c->h_pinned) (void)hipHostFree(c->h_pinned);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
@@ -924,11 +953,9 @@ int ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* log
     // A fresh cache per window (perplexity.rs:69-70).  The token history
     // restarts with the position: every head step appends to it, and it
     // holds max_pos + 1 entries.
-    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
-    c->seq_len = 0;
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
-    int st = ctx_forward(c, ids, burn);
+    int st = ctx_reset(c);
+    if (st) return st;
+    st = ctx_forward(c, ids, burn);
     if (st) return st;
     // ctx_forward synchronized before staging the burn-in ids; the window
     // goes to the device behind the prefill on the same stream.
@@ -937,7 +964,9 @@ int ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* log
     // taken from the logits in place, and the same id is fed to the next
     // decode step from device memory.
     for (size_t i = burn; i < n; i++) {
-        if ((st = launch_log_softmax_at(c->stream, c->logits, V, c->d_sids + i, c->d_logp + (i - burn)))) return st;
+        if ((st = launch_log_softmax_at(c->stream, c->logits, V, c->d_sids + i, c->d_logp + (i - burn),
+                                        c->d_id_error)))
+            return st;
         if (i + 1 < n) {
             if ((st = launch_copy_i32(c->stream, (const int*)(c->d_sids + i), (int*)c->d_token))) return st;
             if ((st = run_decode_step(c))) return st;
@@ -953,12 +982,10 @@ int ctx_score(sq_ctx* c, const uint32_t* ids, size_t n, size_t burn, double* log
 
 int ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms) {
     if (n < 2) return set_error(SQ_ERR_ARG, "prefill_phases: needs a prompt of at least 2 tokens");
-    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
-    c->seq_len = 0;
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
+    int st = ctx_reset(c);
+    if (st) return st;
     c->prof = true;
-    int st = ctx_forward(c, ids, n);
+    st = ctx_forward(c, ids, n);
     c->prof = false;
     hipError_t e = hipStreamSynchronize(c->stream);
     for (int k = 0; k < 4; k++) ms[k] = 0.0;
@@ -1016,10 +1043,7 @@ int ctx_generate(sq_ctx* c, const uint32_t* prompt, size_t n_prompt, size_t max_
     const uint32_t eos = c->m->cfg.eos;
     const bool ignore_eos = flags & SQ_GEN_IGNORE_EOS;
     // A fresh context per generation (text_generator.rs:58).
-    SQ_HIP_CHECK(hipStreamSynchronize(c->stream));
-    c->seq_len = 0;
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_pos, 0, 4, c->stream));
-    SQ_HIP_CHECK(hipMemsetAsync(c->d_nhist, 0, 4, c->stream));
+    if (int st = ctx_reset(c)) return st;
     if (max_tokens == 0) return 0;
 
     if (flags & SQ_GEN_NO_KV_CACHE) {

@@ -130,6 +130,10 @@ struct sq_ctx {
     int* s_error = nullptr;
     unsigned long long* s_trace = nullptr;  // step timeline when enabled
 
+    // Set by a kernel that met a token id past the embedding table (the
+    // reference's slice index panics there, embedding.rs:43-44); the read
+    // itself is clamped in bounds.  Checked by ctx_check, cleared by reset.
+    uint32_t* d_id_error = nullptr;
     uint32_t* d_sids = nullptr;    // the window being scored [max_pos + 1]
     double* d_logp = nullptr;      // its log-probabilities [max_pos + 1]
     uint32_t* h_pinned = nullptr;  // pinned staging for ids / tokens
@@ -181,8 +185,14 @@ int ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms);
 // Host copy of the most recent forward's quantized activations as GGUF
 // Q8_0 blocks: per layer, per site, rows x k/32 blocks; then the LM-head row.
 int ctx_read_taps(sq_ctx* c, void* blocks, size_t n_blocks);
-// Status of the persistent decode step's error word (synchronizes the stream).
+// Status of the device error words: a token id past the embedding table, and
+// the persistent decode step's wait limit (synchronizes the stream).
 int ctx_check(sq_ctx* c);
+// A fresh sequence on the context (ModelContext::clear, context.rs:9-27):
+// position 0, empty token history, device error words cleared and, for the
+// persistent step, the tag epoch moved past every tag an abandoned step may
+// have written.  Synchronizes the stream.
+int ctx_reset(sq_ctx* c);
 int model_load(const char* path, sq_model** out);
 // Parse + config + tensor checks only (no device allocation).
 int model_inspect(const char* path, sq_model** out);

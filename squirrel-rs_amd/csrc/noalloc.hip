@@ -2,8 +2,8 @@
 //
 // sq_linear allocates its scratch (the Q8_0 activation payload and block
 // scales, and the partial tiles of a K split) with hipMalloc on every call.
-// Callers that cannot allocate -- code under HIP graph capture, tight serving
-// loops, harnesses that forbid it -- use this variant: its scratch is one
+// Callers that cannot allocate -- tight serving loops, harnesses that forbid
+// it -- use this variant: its scratch is one
 // file-scope device array, `scratch`, held by each GPU the library runs on
 // until the process ends.  The kernels and their launch shapes are
 // sq_linear's, with the same K-split workspace size, so both entry points
@@ -13,7 +13,8 @@
 // device (with that device current) looks up the device copy's address with
 // hipGetSymbolAddress and keeps it per device; every kernel argument uses
 // that address.  Every call on a GPU shares that GPU's array, so calls that
-// overlap on one GPU race; each call is synchronous.  No part of the scratch
+// overlap on one GPU race.  Each call launches on the null stream and
+// synchronizes it, so it cannot be recorded under a stream capture.  No part of the scratch
 // needs to start at zero: the quantizer writes every activation block it
 // produces and a K split writes every partial tile it sums.
 #include <mutex>

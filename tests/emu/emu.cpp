@@ -9,7 +9,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <deque>
 #include <map>
+#include <memory>
+#include <set>
 #include <vector>
 
 #if defined(__has_feature)
@@ -313,24 +316,90 @@ void run_grid(dim3 grid, dim3 block, size_t dyn_bytes, const std::function<void(
     g_cur = -1;
 }
 
-namespace {
-bool g_capturing = false;
-std::vector<Task>* g_capture = nullptr;
-}  // namespace
-
-bool capturing() { return g_capturing; }
-
-void submit(Task t) {
-    if (g_capturing) {
-        g_capture->push_back(std::move(t));
-        return;
-    }
-    t();
-}
-
 }  // namespace sqemu
 
+// ------------------------------------------------------------------ streams
+// Streams are asynchronous as on the device: every copy, fill, launch and
+// event record is queued on its stream and runs only at a synchronization
+// point that covers that stream (hipStreamSynchronize, hipDeviceSynchronize,
+// hipEventSynchronize, and the implicit ones below), in stream order.  So a
+// host buffer rewritten before the copy that reads it has run, a result read
+// before its producer has run, or work ordered only by the legacy null
+// stream against a non-blocking stream shows up here as wrong data.
+//  * The null stream synchronizes with blocking streams (work queued on one
+//    first drains the other) but not with streams created with
+//    hipStreamNonBlocking.
+//  * hipMemcpy runs on the null stream.  It returns when it is done, except
+//    from pageable host memory to the device, where it returns once the
+//    source is staged and the transfer stays queued on the null stream.
+//    hipMemset is queued on the null stream (asynchronous for device memory).
+//  * hipFree and hipHostFree synchronize the device first.
+//  * hipMemcpyAsync from pinned host memory (hipHostMalloc) reads the source
+//    when the copy runs; from pageable memory it is staged when called.  Into
+//    pinned memory the destination keeps its old contents until the copy
+//    runs; into pageable memory the call drains the stream and copies at once.
+struct sqemu_stream {
+    bool nonblocking = false;
+    bool capturing = false;
+    std::deque<sqemu::Task> q;
+    std::vector<sqemu::Task>* capture = nullptr;
+};
+
 namespace sqemu {
+namespace {
+sqemu_stream g_null_stream;
+std::set<sqemu_stream*> g_streams;
+bool g_draining = false;
+
+sqemu_stream* S(hipStream_t s) { return s ? s : &g_null_stream; }
+
+void drain_one(sqemu_stream* st) {
+    if (g_draining) fatal("a queued operation synchronized a stream");
+    g_draining = true;
+    while (!st->q.empty()) {
+        Task t = std::move(st->q.front());
+        st->q.pop_front();
+        t();
+    }
+    g_draining = false;
+}
+
+void drain_blocking() {
+    for (sqemu_stream* st : g_streams)
+        if (!st->nonblocking) drain_one(st);
+}
+}  // namespace
+
+void drain(hipStream_t s) {
+    sqemu_stream* st = S(s);
+    if (st == &g_null_stream) drain_blocking();
+    drain_one(st);
+}
+
+void drain_all() {
+    drain_one(&g_null_stream);
+    for (sqemu_stream* st : g_streams) drain_one(st);
+}
+
+bool capturing() {
+    if (g_null_stream.capturing) return true;
+    for (sqemu_stream* st : g_streams)
+        if (st->capturing) return true;
+    return false;
+}
+
+void submit(hipStream_t s, Task t) {
+    sqemu_stream* st = S(s);
+    if (st->capturing) {
+        st->capture->push_back(std::move(t));
+        return;
+    }
+    // legacy null-stream ordering against the blocking streams
+    if (st == &g_null_stream) drain_blocking();
+    else if (!st->nonblocking) drain_one(&g_null_stream);
+    st->q.push_back(std::move(t));
+}
+
 // Live device allocations (hipMalloc, hipHostMalloc, device symbols): base -> bytes.
 std::map<uintptr_t, size_t> g_dev;
 
@@ -397,15 +466,27 @@ void check_copy(const char* what, const void* d, const void* s, size_t n, hipMem
 }  // namespace sqemu
 
 // ------------------------------------------------------------------ runtime API
-struct sqemu_stream {
-    int dummy;
-};
 struct sqemu_event {
     std::chrono::steady_clock::time_point t;
+    sqemu_stream* stream = nullptr;
+    bool done = true;
 };
 struct sqemu_graph {
     std::vector<sqemu::Task> tasks;
 };
+
+namespace sqemu {
+// Pinned host allocations (hipHostMalloc): base -> bytes.
+std::map<uintptr_t, size_t> g_pinned;
+namespace {
+bool pinned(const void* p, size_t n) {
+    auto it = g_pinned.upper_bound((uintptr_t)p);
+    if (it == g_pinned.begin()) return false;
+    --it;
+    return (uintptr_t)p + n <= it->first + it->second;
+}
+}  // namespace
+}  // namespace sqemu
 
 hipError_t hipGetLastError() { return hipSuccess; }
 hipError_t hipPeekAtLastError() { return hipSuccess; }
@@ -429,8 +510,15 @@ hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int) {
     }
     return hipSuccess;
 }
-hipError_t hipDeviceSynchronize() { return hipSuccess; }
+hipError_t hipDeviceSynchronize() {
+    sqemu::drain_all();
+    return hipSuccess;
+}
+namespace sqemu {
+uint64_t g_malloc_calls = 0;
+}
 hipError_t hipMalloc(void** p, size_t n) {
+    sqemu::g_malloc_calls++;
     // exact-size heap blocks: the sanitizer poisons everything past n
     void* q = nullptr;
     if (posix_memalign(&q, 256, n ? n : 1)) return hipErrorOutOfMemory;
@@ -441,83 +529,144 @@ hipError_t hipMalloc(void** p, size_t n) {
     return hipSuccess;
 }
 hipError_t hipFree(void* p) {
+    // an implicit device synchronization, as on the device
+    sqemu::drain_all();
     if (p && !sqemu::g_dev.erase((uintptr_t)p)) sqemu::fatal("hipFree of %p, not a device allocation", p);
+    sqemu::g_pinned.erase((uintptr_t)p);
     free(p);
     return hipSuccess;
 }
-hipError_t hipHostMalloc(void** p, size_t n, unsigned) { return hipMalloc(p, n); }
+hipError_t hipHostMalloc(void** p, size_t n, unsigned) {
+    hipError_t e = hipMalloc(p, n);
+    if (e == hipSuccess) sqemu::g_pinned[(uintptr_t)*p] = n;
+    return e;
+}
 hipError_t hipHostFree(void* p) { return hipFree(p); }
 hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind k) {
+    if (sqemu::capturing()) sqemu::fatal("hipMemcpy during a stream capture");
+    if (k == hipMemcpyHostToDevice && !sqemu::pinned(s, n)) {
+        // from pageable memory the call returns once the source is staged;
+        // the transfer itself is null-stream work, so a non-blocking stream
+        // is not ordered after it
+        auto staged = std::make_shared<std::vector<char>>((const char*)s, (const char*)s + n);
+        sqemu::submit(nullptr, [=]() {
+            sqemu::check_copy("hipMemcpy", d, s, n, k);
+            if (n) memcpy(d, staged->data(), n);
+        });
+        return hipSuccess;
+    }
+    // on the null stream: ordered after its own work and the blocking
+    // streams', not after non-blocking streams
+    sqemu::drain(nullptr);
     sqemu::check_copy("hipMemcpy", d, s, n, k);
     if (n) memcpy(d, s, n);
     return hipSuccess;
 }
-hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t) {
-    sqemu::submit([=]() {
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t st) {
+    if (k == hipMemcpyHostToDevice && !sqemu::pinned(s, n) && !(st ? st->capturing : false)) {
+        // pageable source: staged at the call
+        auto staged = std::make_shared<std::vector<char>>((const char*)s, (const char*)s + n);
+        sqemu::submit(st, [=]() {
+            sqemu::check_copy("hipMemcpyAsync", d, s, n, k);
+            if (n) memcpy(d, staged->data(), n);
+        });
+        return hipSuccess;
+    }
+    if (k == hipMemcpyDeviceToHost && !sqemu::pinned(d, n) && !(st ? st->capturing : false)) {
+        // pageable destination: the call returns once the copy is done
+        sqemu::submit(st, [=]() {
+            sqemu::check_copy("hipMemcpyAsync", d, s, n, k);
+            if (n) memmove(d, s, n);
+        });
+        sqemu::drain(st);
+        return hipSuccess;
+    }
+    sqemu::submit(st, [=]() {
         sqemu::check_copy("hipMemcpyAsync", d, s, n, k);
         if (n) memmove(d, s, n);
     });
     return hipSuccess;
 }
 hipError_t hipMemset(void* d, int v, size_t n) {
-    sqemu::check_copy("hipMemset", d, nullptr, n, hipMemcpyHostToDevice);
-    if (n) memset(d, v, n);
+    if (sqemu::capturing()) sqemu::fatal("hipMemset during a stream capture");
+    sqemu::submit(nullptr, [=]() {
+        sqemu::check_copy("hipMemset", d, nullptr, n, hipMemcpyHostToDevice);
+        if (n) memset(d, v, n);
+    });
     return hipSuccess;
 }
-hipError_t hipMemsetAsync(void* d, int v, size_t n, hipStream_t) {
-    sqemu::submit([=]() {
+hipError_t hipMemsetAsync(void* d, int v, size_t n, hipStream_t st) {
+    sqemu::submit(st, [=]() {
         sqemu::check_copy("hipMemsetAsync", d, nullptr, n, hipMemcpyHostToDevice);
         if (n) memset(d, v, n);
     });
     return hipSuccess;
 }
-hipError_t hipStreamCreate(hipStream_t* s) {
-    *s = new sqemu_stream{0};
+hipError_t hipStreamCreate(hipStream_t* s) { return hipStreamCreateWithFlags(s, hipStreamDefault); }
+hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned flags) {
+    *s = new sqemu_stream();
+    (*s)->nonblocking = (flags & hipStreamNonBlocking) != 0;
+    sqemu::g_streams.insert(*s);
     return hipSuccess;
 }
-hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) { return hipStreamCreate(s); }
 hipError_t hipStreamDestroy(hipStream_t s) {
+    // queued work still completes
+    sqemu::drain(s);
+    sqemu::g_streams.erase(s);
     delete s;
     return hipSuccess;
 }
-hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+hipError_t hipStreamSynchronize(hipStream_t s) {
+    sqemu::drain(s);
+    return hipSuccess;
+}
 hipError_t hipEventCreate(hipEvent_t* e) {
-    *e = new sqemu_event{std::chrono::steady_clock::now()};
+    *e = new sqemu_event{std::chrono::steady_clock::now(), nullptr, true};
     return hipSuccess;
 }
 hipError_t hipEventDestroy(hipEvent_t e) {
     delete e;
     return hipSuccess;
 }
-hipError_t hipEventRecord(hipEvent_t e, hipStream_t) {
-    sqemu::submit([e]() { e->t = std::chrono::steady_clock::now(); });
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t s) {
+    e->stream = s ? s : nullptr;
+    e->done = false;
+    sqemu::submit(s, [e]() {
+        e->t = std::chrono::steady_clock::now();
+        e->done = true;
+    });
     return hipSuccess;
 }
-hipError_t hipEventSynchronize(hipEvent_t) { return hipSuccess; }
+hipError_t hipEventSynchronize(hipEvent_t e) {
+    sqemu::drain(e->stream);
+    return hipSuccess;
+}
 hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b) {
+    if (!a->done || !b->done) return hipErrorNotReady;
     *ms = std::chrono::duration<float, std::milli>(b->t - a->t).count();
     return hipSuccess;
 }
-hipError_t hipStreamBeginCapture(hipStream_t, hipStreamCaptureMode) {
-    if (sqemu::g_capturing) return hipErrorInvalidValue;
-    sqemu::g_capturing = true;
-    sqemu::g_capture = new std::vector<sqemu::Task>();
+hipError_t hipStreamBeginCapture(hipStream_t s, hipStreamCaptureMode) {
+    sqemu_stream* st = s ? s : nullptr;
+    if (!st || st->capturing) return hipErrorInvalidValue;
+    st->capturing = true;
+    st->capture = new std::vector<sqemu::Task>();
     return hipSuccess;
 }
-hipError_t hipStreamEndCapture(hipStream_t, hipGraph_t* g) {
-    if (!sqemu::g_capturing) return hipErrorInvalidValue;
-    sqemu::g_capturing = false;
-    *g = new sqemu_graph{std::move(*sqemu::g_capture)};
-    delete sqemu::g_capture;
-    sqemu::g_capture = nullptr;
+hipError_t hipStreamEndCapture(hipStream_t s, hipGraph_t* g) {
+    if (!s || !s->capturing) return hipErrorInvalidValue;
+    s->capturing = false;
+    *g = new sqemu_graph{std::move(*s->capture)};
+    delete s->capture;
+    s->capture = nullptr;
     return hipSuccess;
 }
 hipError_t hipGraphInstantiate(hipGraphExec_t* e, hipGraph_t g, hipGraphNode_t*, char*, size_t) {
     *e = new sqemu_graph{g->tasks};
     return hipSuccess;
 }
-hipError_t hipGraphLaunch(hipGraphExec_t e, hipStream_t) {
-    for (auto& t : e->tasks) sqemu::submit(t);
+hipError_t hipGraphLaunch(hipGraphExec_t e, hipStream_t s) {
+    for (auto& t : e->tasks) sqemu::submit(s, t);
     return hipSuccess;
 }
 hipError_t hipGraphExecDestroy(hipGraphExec_t e) {
@@ -528,15 +677,8 @@ hipError_t hipGraphDestroy(hipGraph_t g) {
     delete g;
     return hipSuccess;
 }
-hipError_t hipGetSymbolAddress(void** p, const void* sym) {
-    *p = const_cast<void*>(sym);
-    size_t bytes = 1;
-#ifdef SQEMU_ASAN
-    char name[64];
-    void* base = nullptr;
-    size_t size = 0;
-    if (!strcmp(__asan_locate_address(*p, name, sizeof name, &base, &size), "global") && base == *p) bytes = size;
-#endif
-    sqemu::g_dev[(uintptr_t)*p] = bytes;
+hipError_t hipGetSymbolAddress(void** p, sqemu_symbol sym) {
+    *p = const_cast<void*>(sym.p);
+    sqemu::g_dev[(uintptr_t)*p] = sym.bytes;
     return hipSuccess;
 }

@@ -20,6 +20,10 @@
 #include "../../oracle/oracle.h"
 #include "gguf.h"
 
+namespace sqemu {
+extern uint64_t g_malloc_calls;  // hipMalloc calls so far (tests/emu/emu.cpp)
+}
+
 static void die(const char* what, int st) {
     fprintf(stderr, "%s failed: %d %s\n", what, st, sq_last_error());
     exit(2);
@@ -96,6 +100,58 @@ int main(int argc, char** argv) {
                got[0], want[0]);
         return 0;
     }
+    if (argc == 2 && std::string(argv[1]) == "--noalloc-count") {
+        // hipMalloc calls made by warm calls of sq_linear_noalloc on its two
+        // paths (m = 1: the matvec; m = 67: the K-split matmul), next to
+        // sq_linear's for the same calls
+        const int k = 2048, n = 256;
+        std::vector<uint8_t> w((size_t)n * (k / 32) * 34);
+        for (size_t i = 0; i < w.size(); i++) w[i] = (uint8_t)(i * 131 + 7);
+        for (size_t b = 0; b < (size_t)n * (k / 32); b++) {
+            const uint16_t d = or_f32_to_f16(0.001f);
+            memcpy(w.data() + b * 34, &d, 2);
+        }
+        sq_weight* W = nullptr;
+        int st = sq_weight_upload(SQ_Q8_0, w.data(), n, k, &W);
+        if (st) die("sq_weight_upload", st);
+        float *dx = nullptr, *dy = nullptr;
+        sq_malloc((void**)&dx, (size_t)67 * k * 4);
+        sq_malloc((void**)&dy, (size_t)67 * n * 4);
+        std::vector<float> x((size_t)67 * k, 0.5f);
+        sq_memcpy_h2d(dx, x.data(), x.size() * 4);
+        for (int m : {1, 67}) {
+            if ((st = sq_linear_noalloc(dx, m, k, W, dy, 0))) die("sq_linear_noalloc", st);  // warm
+            const uint64_t a0 = sqemu::g_malloc_calls;
+            if ((st = sq_linear_noalloc(dx, m, k, W, dy, 0))) die("sq_linear_noalloc", st);
+            const uint64_t a1 = sqemu::g_malloc_calls;
+            if ((st = sq_linear(dx, m, k, W, dy, 0))) die("sq_linear", st);
+            const uint64_t a2 = sqemu::g_malloc_calls;
+            printf("m %d noalloc_mallocs %llu linear_mallocs %llu\n", m, (unsigned long long)(a1 - a0),
+                   (unsigned long long)(a2 - a1));
+        }
+        return 0;
+    }
+    if (argc == 2 && std::string(argv[1]) == "--embed-guard") {
+        // sq_embed with device ids in and past a 64-row Q8_0 table: the
+        // in-range call succeeds; an id of 64 or of 2^32 - 1 is SQ_ERR_ARG
+        // (the reference panics on the slice index, embedding.rs:43-44),
+        // with every read in bounds
+        const int rows = 64, k = 64;
+        std::vector<uint8_t> w((size_t)rows * (k / 32) * 34, 1);
+        sq_weight* W = nullptr;
+        int st = sq_weight_upload(SQ_Q8_0, w.data(), rows, k, &W);
+        if (st) die("sq_weight_upload", st);
+        uint32_t* d_ids = nullptr;
+        float* d_out = nullptr;
+        sq_malloc((void**)&d_ids, 3 * 4);
+        sq_malloc((void**)&d_out, 3 * k * 4);
+        const uint32_t cases[3][3] = {{3, 63, 0}, {3, 64, 0}, {0xFFFFFFFFu, 1, 2}};
+        for (auto& ids : cases) {
+            sq_memcpy_h2d(d_ids, ids, sizeof(ids));
+            printf("embed ids %u %u %u status %d\n", ids[0], ids[1], ids[2], sq_embed(d_ids, 3, W, d_out));
+        }
+        return 0;
+    }
     if (argc < 8) {
         fprintf(stderr, "usage: emu_model gguf mode flags n_prompt n_decode seed max_pos [generate]\n");
         return 2;
@@ -111,10 +167,18 @@ int main(int argc, char** argv) {
     // that step, change one element of the device's blocks by 2 (kind 0) or
     // one block scale by 1% (kind 1) -- a planted mistake the lock must report
     int cs = -1, cl = 0, csite = 0, ce = 0, ck = 0;
+    // plant=<step>,<layer>,<site>,<quanta>: the oracle's planted systematic
+    // error (or_lock plant_*): that site's blocks as an implementation whose
+    // scaled values are all off by <quanta> would produce them
+    int ps = -1, pl = 0, psite = 0;
+    float pq = 0.0f;
+    float tol = 0.02f;  // tol=<quanta>: the lock's midpoint tolerance
     for (int i = 8; i < argc; i++) {
         const std::string a = argv[i];
         if (a == "generate") gen = true;
         if (a.rfind("corrupt=", 0) == 0) sscanf(a.c_str() + 8, "%d,%d,%d,%d,%d", &cs, &cl, &csite, &ce, &ck);
+        if (a.rfind("plant=", 0) == 0) sscanf(a.c_str() + 6, "%d,%d,%d,%f", &ps, &pl, &psite, &pq);
+        if (a.rfind("tol=", 0) == 0) tol = strtof(a.c_str() + 4, nullptr);
     }
 
     sq_model* m = nullptr;
@@ -196,14 +260,20 @@ int main(int argc, char** argv) {
                 else b.d = or_f32_to_f16(or_f16_to_f32(b.d) * 1.01f);
             }
             lk.blocks = taps.data();
-            lk.tol = 0.02f;
+            lk.tol = tol;
+            if (step == ps) {
+                lk.plant_layer = pl;
+                lk.plant_site = psite;
+                lk.plant_quanta = pq;
+            }
         }
         if ((st = or_forward_locked(&om, oc, p, n, locked ? &lk : nullptr))) die("or_forward", st);
         if (locked)
-            printf("lock step %d values %llu flips %llu scale_flips %llu bad %llu first_bad %d/%d/%zu/%.3g\n", step,
-                   (unsigned long long)lk.values, (unsigned long long)lk.flips, (unsigned long long)lk.scale_flips,
-                   (unsigned long long)lk.bad, lk.first_bad_layer, lk.first_bad_site, lk.first_bad_index,
-                   lk.first_bad_dist);
+            printf("lock step %d values %llu flips %llu scale_flips %llu bad %llu first_bad %d/%d/%zu/%.3g "
+                   "max_flip_dist %.3g max_scale_rel %.3g\n",
+                   step, (unsigned long long)lk.values, (unsigned long long)lk.flips,
+                   (unsigned long long)lk.scale_flips, (unsigned long long)lk.bad, lk.first_bad_layer,
+                   lk.first_bad_site, lk.first_bad_index, lk.first_bad_dist, lk.max_flip_dist, lk.max_scale_rel);
         const float* want = or_ctx_logits(oc);
         double num = 0, den = 0, mx = 0;
         for (uint32_t i = 0; i < info.vocab; i++) {

@@ -66,6 +66,7 @@ enum : int {
     hipErrorInvalidValue = 1,
     hipErrorOutOfMemory = 2,
     hipErrorInvalidConfiguration = 9,
+    hipErrorNotReady = 600,
     hipErrorLaunchFailure = 719,
 };
 struct sqemu_stream;
@@ -86,7 +87,12 @@ enum hipDeviceAttribute_t { hipDeviceAttributeWallClockRate = 1, hipDeviceAttrib
 #define hipStreamNonBlocking 1u
 #define hipStreamDefault 0u
 #define hipHostMallocDefault 0u
-#define HIP_SYMBOL(x) (&(x))
+// a device symbol: its address and size (the device copy is the host object)
+struct sqemu_symbol {
+    const void* p;
+    size_t bytes;
+};
+#define HIP_SYMBOL(x) (sqemu_symbol{(const void*)&(x), sizeof(x)})
 
 // ------------------------------------------------------------------ emulator core
 namespace sqemu {
@@ -111,10 +117,15 @@ void* dyn_lds();
 [[noreturn]] void fatal(const char* fmt, ...);
 
 using Task = std::function<void()>;
-// Runs one launch now, or records it while a stream capture is active.
-void submit(Task t);
+// Queues one operation on a stream (the null stream when s is null), or
+// records it while that stream is capturing.  Queued operations run at the
+// next synchronization point that covers their stream, in stream order.
+void submit(hipStream_t s, Task t);
 void run_grid(dim3 grid, dim3 block, size_t dyn_lds_bytes, const std::function<void()>& body);
 bool capturing();
+// Runs what is queued on a stream (with the null stream's ordering) / on all.
+void drain(hipStream_t s);
+void drain_all();
 
 template <typename T>
 inline uint64_t to_bits(T v) {
@@ -354,9 +365,9 @@ namespace sqemu {
 // dereference, and stops the run.
 void check_kernel_arg(const void* kernel, int index, const void* arg, size_t bytes);
 template <typename... P, typename... A>
-void launch(void (*k)(P...), dim3 grid, dim3 block, size_t shm, hipStream_t, A&&... args) {
+void launch(void (*k)(P...), dim3 grid, dim3 block, size_t shm, hipStream_t stream, A&&... args) {
     auto tup = std::make_tuple(static_cast<std::decay_t<P>>(args)...);
-    submit([=]() {
+    submit(stream, [=]() {
         std::apply(
             [&](const auto&... a) {
                 int i = 0;
@@ -406,4 +417,4 @@ hipError_t hipGraphInstantiate(hipGraphExec_t* e, hipGraph_t g, hipGraphNode_t* 
 hipError_t hipGraphLaunch(hipGraphExec_t e, hipStream_t s);
 hipError_t hipGraphExecDestroy(hipGraphExec_t e);
 hipError_t hipGraphDestroy(hipGraph_t g);
-hipError_t hipGetSymbolAddress(void** p, const void* sym);
+hipError_t hipGetSymbolAddress(void** p, sqemu_symbol sym);

@@ -6,6 +6,11 @@
 // hoststruct` a struct holding one, and `selftest freed` replays a captured
 // launch whose buffer was freed after the capture (each must be refused);
 // `selftest ok` runs the in-bounds twin and prints the sum.
+// Stream timing: `selftest pinned` rewrites a pinned source after queuing its
+// copy and before synchronizing (the copy must see the rewrite: sum 512);
+// `selftest nullstream` reads a non-blocking stream's result with hipMemcpy
+// without synchronizing that stream (the read must miss it: sum 256, not 64);
+// `selftest synced` is the correct twin of the latter (sum 64).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -27,6 +32,10 @@ __global__ void view_kernel(View v, float* out) {
     if (threadIdx.x == 0) *out = v.x[0] + (float)v.n;
 }
 
+__global__ void set_kernel(float* out, float v) {
+    if (threadIdx.x == 0) *out = v;
+}
+
 __global__ void diverge_kernel(float* out) {
     float v = (float)threadIdx.x;
     if (threadIdx.x < 32) v += __shfl_xor(v, 1, 64);
@@ -42,7 +51,24 @@ int main(int argc, char** argv) {
     float h[n];
     for (int i = 0; i < n; i++) h[i] = 1.0f;
     hipMemcpy(x, h, sizeof(h), hipMemcpyHostToDevice);
-    if (!strcmp(what, "diverge")) {
+    if (!strcmp(what, "pinned")) {
+        float* hp = nullptr;
+        hipHostMalloc(&hp, n * sizeof(float), hipHostMallocDefault);
+        for (int i = 0; i < n; i++) hp[i] = 1.0f;
+        hipStream_t s;
+        hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+        hipMemcpyAsync(x, hp, n * sizeof(float), hipMemcpyHostToDevice, s);
+        for (int i = 0; i < n; i++) hp[i] = 2.0f;  // before the copy has run
+        hipLaunchKernelGGL(read_kernel, dim3(1), dim3(64), 0, s, x, n, 0, out);
+        hipStreamSynchronize(s);
+    } else if (!strcmp(what, "nullstream") || !strcmp(what, "synced")) {
+        hipLaunchKernelGGL(read_kernel, dim3(1), dim3(64), 0, nullptr, x, n, 0, out);
+        hipDeviceSynchronize();
+        hipStream_t s;
+        hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+        hipLaunchKernelGGL(set_kernel, dim3(1), dim3(64), 0, s, out, 64.0f);
+        if (!strcmp(what, "synced")) hipStreamSynchronize(s);
+    } else if (!strcmp(what, "diverge")) {
         hipLaunchKernelGGL(diverge_kernel, dim3(1), dim3(64), 0, nullptr, out);
     } else if (!strcmp(what, "host")) {
         hipLaunchKernelGGL(read_kernel, dim3(1), dim3(64), 0, nullptr, (const float*)h, n, 0, out);

@@ -2,7 +2,8 @@
 
 Every kernel except the persistent decode step is compiled for the host
 against an emulated HIP device (one fiber per work-item, cross-lane
-operations as wavefront collectives) with AddressSanitizer, and driven
+operations as wavefront collectives, streams that run their queued copies
+and launches only when synchronized) with AddressSanitizer, and driven
 through the C ABI by tests/emu/emu_model.cpp.  These tests check, without a
 GPU:
   * that the emulator itself catches an out-of-bounds read, a cross-lane
@@ -84,6 +85,41 @@ def test_emulator_catches_out_of_bounds_and_divergence(emu):
     assert oob.returncode != 0 and "heap-buffer-overflow" in oob.stderr
     div = subprocess.run([st, "diverge"], capture_output=True, text=True, env=ENV)
     assert div.returncode != 0 and "cross-lane" in div.stderr
+
+
+@pytest.mark.parametrize("case,want", [("pinned", "sum 512"), ("nullstream", "sum 256"), ("synced", "sum 64")])
+def test_emulator_streams_are_asynchronous(emu, case, want):
+    """Queued copies and launches run only when their stream is synchronized,
+    in stream order: a pinned source rewritten before its copy ran is read as
+    rewritten, and hipMemcpy on the null stream does not wait for a
+    non-blocking stream.  A missing synchronization in the library's host
+    code therefore shows up in the emulated runs as wrong data."""
+    p = subprocess.run([build_emu.SELFTEST, case], capture_output=True, text=True, env=ENV)
+    assert p.returncode == 0 and want in p.stdout, p.stdout + p.stderr
+
+
+def test_noalloc_allocates_nothing(emu):
+    """sq_linear_noalloc's contract: a warm call allocates no device memory,
+    on the single-row matvec path and on the K-split matmul path (sq_linear,
+    beside it, allocates its scratch on every call)."""
+    p = subprocess.run([emu, "--noalloc-count"], capture_output=True, text=True, env=ENV)
+    assert p.returncode == 0 and "AddressSanitizer" not in p.stderr, p.stdout + p.stderr
+    got = {int(m[1]): (int(m[2]), int(m[3]))
+           for m in re.finditer(r"^m (\d+) noalloc_mallocs (\d+) linear_mallocs (\d+)$", p.stdout, re.M)}
+    assert set(got) == {1, 67}, p.stdout
+    for m, (noalloc, linear) in got.items():
+        assert noalloc == 0 and linear > 0, (m, noalloc, linear)
+
+
+def test_device_token_id_past_the_table_is_an_error(emu):
+    """An id past the embedding table that reaches a kernel from device
+    memory (the host validates the ids it is given) is an error status, as
+    the reference's slice index panics (embedding.rs:43-44), and the row read
+    stays in bounds (AddressSanitizer watches every access here)."""
+    p = subprocess.run([emu, "--embed-guard"], capture_output=True, text=True, env=ENV)
+    assert p.returncode == 0 and "AddressSanitizer" not in p.stderr, p.stdout + p.stderr
+    got = re.findall(r"^embed ids (\d+) (\d+) (\d+) status (\d+)$", p.stdout, re.M)
+    assert got == [("3", "63", "0", "0"), ("3", "64", "0", "22"), ("4294967295", "1", "2", "22")], p.stdout
 
 
 @pytest.mark.parametrize("case,where", [("host", "stack"), ("hoststruct", "stack"), ("freed", "heap")])

@@ -89,6 +89,31 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a.astype(np.float64) - b) / np.linalg.norm(b))
 
 
+def lock_summary(label, rows):
+    """Prints, and appends to the JSON-lines file named by SQ_LOCK_STATS when
+    set, what the lock accepted over a run: flips per site kind and overall,
+    the largest accepted distance of a flipped element from its rounding
+    midpoint (quanta) and of a flipped scale from its midpoint (relative)."""
+    import json
+    sv = np.sum([r[3]["site_values"] for r in rows], axis=0)
+    sf = np.sum([r[3]["site_flips"] for r in rows], axis=0)
+    rec = {"label": label, "steps": len(rows), "values": int(sum(r[3]["values"] for r in rows)),
+           "flips": int(sum(r[3]["flips"] for r in rows)),
+           "scale_flips": int(sum(r[3]["scale_flips"] for r in rows)),
+           "max_flip_dist": max(r[3]["max_flip_dist"] for r in rows),
+           "max_scale_rel": max(r[3]["max_scale_rel"] for r in rows),
+           "max_step_flip_rate": max(r[3]["flips"] / max(1, r[3]["values"]) for r in rows),
+           "site_flip_rate": [float(f) / max(1, float(v)) for f, v in zip(sf, sv)],
+           "max_rel_l2": max(r[1] for r in rows)}
+    print(f"{label}: {rec['steps']} steps, {rec['values']} activations compared, {rec['flips']} boundary flips, "
+          f"{rec['scale_flips']} scale flips; largest accepted flip {rec['max_flip_dist']:.2e} quanta from a "
+          f"midpoint, scale {rec['max_scale_rel']:.2e}; worst step flip rate {rec['max_step_flip_rate']:.2e}; "
+          f"rel_l2 max {rec['max_rel_l2']:.2e}")
+    if os.environ.get("SQ_LOCK_STATS"):
+        with open(os.environ["SQ_LOCK_STATS"], "a") as f:
+            f.write(json.dumps(rec) + "\n")
+
+
 def check_logits(path, seq, got, blocks, label, max_pos=256):
     """Phase-locked comparison of the integer path (see the module doc)."""
     om = O.OracleModel(path)
@@ -98,10 +123,7 @@ def check_logits(path, seq, got, blocks, label, max_pos=256):
         st = oc.forward(ids, lock=blk, tol=LOCK_TOL)
         w = oc.logits()
         rows.append((step, rel_l2(g, w), float(np.abs(g - w).max()), st))
-    n_flips = sum(r[3]["flips"] for r in rows)
-    n_vals = sum(r[3]["values"] for r in rows)
-    print(f"{label}: {len(rows)} steps, {n_vals} activations compared, {n_flips} boundary flips, "
-          f"{sum(r[3]['scale_flips'] for r in rows)} scale flips; rel_l2 max {max(r[1] for r in rows):.2e}")
+    lock_summary(label, rows)
     for step, e, mx, st in rows:
         assert st["bad"] == 0, f"step {step}: {st['bad']} bad blocks, first (layer, site, index, dist) {st['first_bad']}"
         assert st["flips"] <= FLIP_RATE * st["values"], f"step {step}: {st['flips']} flips of {st['values']}"
@@ -579,25 +601,43 @@ def test_full_size_q8_0_prompt_32_decode_63(model_dir):
 
 
 @FULL
-def test_full_size_q4_0_prompt_128(model_dir):
-    """Llama-3.2-1B, Q4_0: a 128-token prefill, then 8 decode steps."""
-    check_full(full_model(model_dir, "Q4_0"), full_seq(128, 8, 1), "1B Q4_0 128+8", max_pos=192)
+def test_full_size_q4_0_prompt_128_decode_255(model_dir):
+    """Llama-3.2-1B, Q4_0, the whole 256-token workload: a 128-token
+    prefill, then all 255 decode steps (positions 128..382), teacher-forced."""
+    check_full(full_model(model_dir, "Q4_0"), full_seq(128, 255, 1), "1B Q4_0 128+255", max_pos=384)
+
+
+# The long-context and prefill workloads run at the 1B widths with 2 of the
+# 16 layers.  Every layer runs the same kernels and instances on the same
+# shapes (the layer index only selects the weights and the KV-cache slice),
+# and the 16-layer depth is covered by the two full-size tests above; what
+# these two workloads add -- 4096+ cached positions, and a 2048-token
+# batched prefill -- is fully exercised by any one layer, while the oracle's
+# row-serial prefill of 16 layers at these lengths would take minutes.
 
 
 @FULL
 def test_full_width_long_context_decode(model_dir):
-    """1B widths (2 layers) at 4100 positions: a 4092-token prefill, then
-    decode steps at positions 4092..4099.  On the full 256-CU grid the
-    persistent step gives each (KV head, chunk) item 3 tiles of 64 positions
-    (65 tiles, 8 KV heads) and then merges the chunks."""
-    check_full(full_model(model_dir, "Q8_0", n_layers=2), full_seq(4092, 8, 2), "1B-wide long context",
-               max_pos=4104)
+    """1B widths (2 layers), the long-context workload's whole length: a
+    4096-token prefill, then all 127 decode steps (positions 4096..4222).  On
+    the full 256-CU grid the persistent step gives each (KV head, chunk) item
+    3 tiles of 64 positions (65-67 tiles, 8 KV heads) and then merges the
+    chunks."""
+    check_full(full_model(model_dir, "Q8_0", n_layers=2), full_seq(4096, 127, 2), "1B-wide long context 4096+127",
+               max_pos=4232)
 
 
 @FULL
 def test_full_width_prefill_2048(model_dir):
     """1B widths (2 layers): a 2048-token batched prefill -- every matmul on
-    the matrix cores without a K split (32 x 32..256 output tiles), causal
-    attention over 2048 x 2048 per head -- then 2 decode steps."""
-    check_full(full_model(model_dir, "Q8_0", n_layers=2), full_seq(2048, 2, 3), "1B-wide prefill 2048",
-               max_pos=2056)
+    the full-rate matrix-core kernel without a K split: per layer the gate/up
+    projection on 128 x 128 tiles (2048 tiles) and the QKV, o and down
+    projections on 128 x 64 tiles (768, 512, 512), causal attention over
+    2048 x 2048 per head -- then the workload's 15 decode steps."""
+    from sqhip import ops
+    ops.gemm_counters(reset=True)
+    check_full(full_model(model_dir, "Q8_0", n_layers=2), full_seq(2048, 15, 3), "1B-wide prefill 2048+15",
+               max_pos=2064)
+    n = ops.gemm_counters(reset=True)
+    assert n == {"launches": 8, "split_launches": 0, "tile128_launches": 2, "max_splits": 1,
+                 "tile128x64_launches": 6}, n

@@ -390,3 +390,20 @@ def test_embed_bit_exact(wtype):
     ops.embed(DeviceArray.from_numpy(toks), ops.Weight(wtype, w, vocab, dim), out)
     want = O.embed(toks, wtype, w, dim, vocab)
     assert np.array_equal(out.numpy(), want)
+
+
+@pytest.mark.parametrize("bad", [300, 2**31, 2**32 - 1])
+def test_embed_id_past_the_table_is_an_error(bad):
+    """A token id past the table that reaches the kernel from device memory
+    is an error status, as the reference's slice index panics
+    (embedding.rs:43-44).  The kernel clamps the row it reads, so the launch
+    stays in bounds, and raises the error word the host turns into the
+    status."""
+    vocab, dim = 300, 2048
+    w, _ = quant_weights(O.Q8_0, vocab, dim, seed=11)
+    table = ops.Weight(O.Q8_0, w, vocab, dim)
+    out = DeviceArray((3, dim))
+    ops.embed(DeviceArray.from_numpy(np.array([3, 299, 0], np.uint32)), table, out)
+    with pytest.raises(sq.SqError) as e:
+        ops.embed(DeviceArray.from_numpy(np.array([3, bad, 0], np.uint32)), table, out)
+    assert e.value.code == 22 and "embedding table" in str(e.value)
