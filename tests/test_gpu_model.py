@@ -33,9 +33,9 @@ pytestmark = pytest.mark.gpu
 
 sq = pytest.importorskip("sqhip")
 
-LOCK_TOL = 0.02     # quanta from a rounding midpoint within which a flip is accepted
+from lock_bar import FLIP_RATE, LOCK_TOL  # noqa: E402
+
 LOGIT_REL = 1e-5    # rel_l2 of the logits under the lock (f32 summation order only)
-FLIP_RATE = 0.01    # accepted flips per compared activation (sanity bound)
 LOGIT_ABS_FLOOR = 2e-4
 MODES = {"Q8_0": O.W8A8, "Q4_0": O.W8A8, "BF16": O.W8A32}
 A32_SKIP = ("f32-activation kernels (BF16, SQUIRREL_F32_ACTS) are switched off after a GPU "
@@ -126,8 +126,10 @@ def check_logits(path, seq, got, blocks, label, max_pos=256):
     lock_summary(label, rows)
     for step, e, mx, st in rows:
         assert st["bad"] == 0, f"step {step}: {st['bad']} bad blocks, first (layer, site, index, dist) {st['first_bad']}"
-        assert st["flips"] <= FLIP_RATE * st["values"], f"step {step}: {st['flips']} flips of {st['values']}"
         assert e <= LOGIT_REL, f"step {step}: rel_l2 {e:.3e} > {LOGIT_REL} (max|d| {mx:.2e})"
+    rate = FLIP_RATE["Q4_0" if om.s.wtype == O.Q4_0 else "Q8_0"]
+    flips, values = sum(r[3]["flips"] for r in rows), sum(r[3]["values"] for r in rows)
+    assert flips <= rate * values, f"{flips} flips of {values} activations (bar {rate:.1e})"
     return rows
 
 
@@ -352,9 +354,12 @@ def test_persistent_matches_multi_kernel_generation(tiny_gguf):
 
 @pytest.mark.parametrize("wtype", ["Q8_0", "BF16"])
 def test_generate_matches_forward_loop(tiny_gguf, wtype):
-    """TextTokenGenerator::generate == forward/sample loop, and the greedy
-    sequence vs the oracle's (first divergence reported, not asserted beyond
-    the steps whose top-2 margin exceeds the logit tolerance)."""
+    """TextTokenGenerator::generate == the forward/sample loop, and every
+    token of that free-running greedy sequence is the oracle's greedy pick:
+    the oracle follows the device's tokens, locked to its quantized
+    activations at every step, so the two sides' logits differ by f32
+    summation order only; a pick may differ only where the oracle's top-2
+    margin is within twice the largest logit difference of that step."""
     if wtype == "BF16":
         pytest.skip(A32_SKIP)
     path = tiny_gguf(wtype, "g4")
@@ -364,26 +369,26 @@ def test_generate_matches_forward_loop(tiny_gguf, wtype):
     gen, ms = sq.TextTokenGenerator(m, c).generate(prompt, 20, ignore_eos=True)
     assert len(gen) == 20 and np.all(ms > 0)
     c2 = m.new_context(128)
-    c2.forward(prompt)
-    loop = [c2.argmax()]
-    for _ in range(19):
-        c2.forward([loop[-1]])
-        loop.append(c2.argmax())
-    assert gen == loop
-    om = O.OracleModel(path)
-    oc = om.new_context(128, MODES[wtype])
-    oc.forward(prompt)
-    ref = []
+    c2.act_taps(True)
+    oc = O.OracleModel(path).new_context(128, MODES[wtype])
+    loop, ids, agree = [], prompt, 0
     for step in range(20):
-        lg = oc.logits()
-        ref.append(O.greedy(lg))
-        srt = np.sort(lg)
-        if ref[-1] != gen[step]:
-            margin = float(srt[-1] - srt[-2])
-            print(f"greedy diverges at step {step} (oracle top-2 margin {margin:.2e})")
-            assert margin <= 0.1
-            break
-        oc.forward([ref[-1]])
+        c2.forward(ids)
+        tok = c2.argmax()
+        loop.append(tok)
+        st = oc.forward(ids, lock=c2.act_tap_blocks(), tol=LOCK_TOL)
+        g, w = c2.logits(), oc.logits()
+        assert st["bad"] == 0 and rel_l2(g, w) <= LOGIT_REL, f"step {step}"
+        if O.greedy(w) != tok:
+            srt = np.sort(w)
+            margin, noise = float(srt[-1] - srt[-2]), float(np.abs(g - w).max())
+            print(f"step {step}: oracle picks {O.greedy(w)}, device {tok}, top-2 margin {margin:.2e}")
+            assert margin <= 2 * noise, f"step {step}: margin {margin:.2e} vs logit difference {noise:.2e}"
+        else:
+            agree += 1
+        ids = [tok]
+    print(f"{wtype}: {agree} of 20 free-running greedy picks equal the oracle's")
+    assert gen == loop
 
 
 def test_eos_stops_generation(tiny_gguf, model_dir):

@@ -187,6 +187,38 @@ def test_matmul_tiles_agree(wtype, monkeypatch):
     assert np.all(err <= 4e-6 * term_mag(x[rows], wf) + 1e-6)
 
 
+@pytest.mark.parametrize("tile", ["64", "128x64", "128"])
+def test_matmul_subnormal_activation_scales(tile, monkeypatch):
+    """Activation rows of magnitude about 1e-4 have Q8_0 block scales below
+    binary16's smallest normal (6.1e-5): the matrix-core kernels form the
+    scale product sa * sw from f16 operands, so a flush of subnormal inputs
+    would zero these outputs.  Every output must match the oracle within
+    4e-6 of its sum of |terms|, with no absolute floor, on each tiling."""
+    m, k, n = 256, 2048, 4096
+    w, _ = quant_weights(O.Q8_0, n, k, seed=91)
+    r = rng(5)
+    x = (r.standard_normal((m, k)) * (1e-4 * r.uniform(0.5, 2.0, (m, 1)))).astype(np.float32)
+    aq = O.quantize_row_q8_0(x.reshape(-1))
+    sa = aq["d"].view(np.float16).astype(np.float32)
+    assert np.all(sa < 6.1e-5) and np.all(sa > 0)
+    W = ops.Weight(O.Q8_0, w, n, k)
+    monkeypatch.setenv("SQUIRREL_GEMM_TILE", tile)
+    out = DeviceArray((m, n))
+    ops.gemm_counters(reset=True)
+    ops.linear(DeviceArray.from_numpy(x), W, out)
+    c = ops.gemm_counters(reset=True)
+    assert c["tile128_launches"] == (1 if tile == "128" else 0) and \
+        c["tile128x64_launches"] == (1 if tile == "128x64" else 0), c
+    got = out.numpy().astype(np.float64)
+    rows = np.arange(0, m, 13)
+    want = O.linear(x[rows], O.Q8_0, w, n, O.W8A8)
+    wf = np.stack([O.dequantize(O.Q8_0, w[i], k) for i in range(n)])
+    mag = term_mag(x[rows], wf)
+    err = np.abs(got[rows] - want)
+    assert np.all(mag > 0)
+    assert np.all(err <= 4e-6 * mag), float((err / mag).max())
+
+
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0, O.BF16])
 def test_linear_shared_matches_separate(wtype):
     """fused_matches_separate_calls (matmul.rs:257-279): bit-equal."""
