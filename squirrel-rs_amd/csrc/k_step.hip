@@ -600,8 +600,8 @@ __device__ __forceinline__ int dpp_int(int v) {
 
 // RMSNorm (rms_norm.rs:40-56) of the hidden row and its Q8_0 quantization
 // (dot_prod.rs:21-31), spread over the compute group: thread t owns elements
-// 8t .. 8t+7 of the row.  They come from the exchange words src[8t ..] once
-// these carry `tag` (or, with src null, from the token's embedding row).  The
+// 8t .. 8t+7 of the row.  They come from the exchange words src[hslot(8t + e)]
+// once these carry `tag` (or, with src null, from the token's embedding row).  The
 // sum of squares is reduced per wavefront, then across the wavefronts in a
 // fixed order after a compute-group barrier; the four threads of a 32-block
 // (a lane quad) agree on its scale through DPP and the blocks land in
@@ -623,8 +623,8 @@ __device__ __forceinline__ bool norm_quant(StepShared& S, const u64* src, unsign
         u64 w[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            p[e] = mine ? src + 8 * t + e : nullptr;
-            w[e] = mine ? ld_c(src + 8 * t + e) : 0;
+            p[e] = mine ? src + e * (D >> 3) + t : nullptr;  // element 8t + e (hslot)
+            w[e] = mine ? ld_c(src + e * (D >> 3) + t) : 0;
         }
         if (!await_words(p, w, tag, C, &S.abort)) lds_st(&S.abort, 1);
 #pragma unroll
@@ -685,6 +685,12 @@ __device__ __forceinline__ bool norm_quant(StepShared& S, const u64* src, unsign
     }
     return csync(S, gen, C);
 }
+
+// Word of the hidden-row exchange X.h that holds element `row`: element
+// 8t + e sits at e * (D / 8) + t, so that compute thread t's eight words
+// (norm_quant) are e * (D / 8) + t for e < 8 -- one coalesced 512-byte run
+// per wavefront and load instead of eight scattered 64-byte pieces.
+__device__ __forceinline__ int hslot(int row, int D) { return (row & 7) * (D >> 3) + (row >> 3); }
 
 // The lane's activation block (block = lane) after norm_quant.
 __device__ __forceinline__ ActQ act_lane(const StepShared& S, int D) {
@@ -1272,7 +1278,7 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                         const int row = g.row0o + cw + NCW * r;
                         if (r < n_own && row < D) {
                             h_own[r] += res[r];  // elementwise_add (layers.rs:81-109)
-                            if (lane == 0) putf(X.h + row, h_own[r], T);
+                            if (lane == 0) putf(X.h + hslot(row, D), h_own[r], T);
                         }
                     }
                 }
@@ -1382,7 +1388,7 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
                         const int row = g.row0o + cw + NCW * r;
                         if (row < D) {
                             h_own[r] += res;
-                            if (lane == 0) putf(X.h + row, h_own[r], T);
+                            if (lane == 0) putf(X.h + hslot(row, D), h_own[r], T);
                         }
                     }
                 }
