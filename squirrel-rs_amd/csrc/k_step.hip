@@ -74,7 +74,10 @@ constexpr int DMAX = 2048;         // model width supported (one 32-block per la
 constexpr int FMAX = 8192;         // FFN width supported
 constexpr int MAXG = 4;            // GQA group size supported (one compute wavefront per head)
 constexpr int RMAX = 2;            // residual rows a compute wavefront owns
-constexpr int HEAD_RING_8THS = 4;  // eighths of a wavefront's LM-head rows that come through the ring
+// eighths of a wavefront's LM-head rows that come through the ring (the
+// rest the compute wavefronts load themselves; Q4_0 rows, half the bytes,
+// measured slower that way and all come through the ring)
+constexpr int head_ring_8ths(int wt) { return wt == WT_Q8_0 ? 4 : 8; }
 constexpr int XMAX = FMAX / 4 + FMAX / 32;  // exchange words gathered at once
 constexpr int WPT = (XMAX + CNT - 1) / CNT;  // ... per compute thread
 
@@ -834,8 +837,14 @@ enum TraceSlot : int {
 // timeline, the activation taps) are compiled in.  A launch that asks for
 // neither runs the instance without them, whose code the compiler lays out
 // better (measured about 3.5% faster per token).
+//
+// Each instance starts on a 4 KB boundary.  The same machine code runs at
+// different speeds depending on where it starts modulo 4 KB (the Q4_0
+// instance between 1991 and 2087 tokens/s for start offsets 0x000-0xf00,
+// Q8_0 within 1%); aligned, an edit to one instance no longer moves the
+// others.
 template <int WT, bool INSTR>
-__global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
+__global__ __launch_bounds__(SNT, 1) __attribute__((aligned(4096))) void decode_step_kernel(StepArgs a) {
     __shared__ StepShared S;
     // the wavefront index is uniform; readfirstlane lets the compiler keep
     // everything derived from it (roles, row loops) in scalar registers
@@ -846,13 +855,17 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
     const int KB = D >> 5;
     const int GQ = a.n_heads / a.n_kv_heads;
     const Ctl C{a.error, a.spin_limit};
-    StreamGeo g = stream_geo(WT, a.n_layers, D, F, QD, KVD, a.vocab, G, wg);
+    StreamGeo g0 = stream_geo(WT, a.n_layers, D, F, QD, KVD, a.vocab, G, wg);
     // The LM head: row i = cw + NCW r of the CU's block is wavefront cw's
     // r-th row.  Rows r < head_nr come through the ring (the block's first
     // NCW head_nr rows, so the loaders stop there); the compute wavefronts
     // load the others themselves, which adds their requests to the loaders'.
-    const int head_nr = ((g.nh + NCW - 1) / NCW * HEAD_RING_8THS + 7) / 8;
-    g.total = a.n_layers * g.LU + min(g.nh, NCW * head_nr) * g.ua;
+    int head_nr = (g0.nh + NCW - 1) / NCW;
+    if constexpr (head_ring_8ths(WT) < 8) {
+        head_nr = (head_nr * head_ring_8ths(WT) + 7) / 8;
+        g0.total = a.n_layers * g0.LU + min(g0.nh, NCW * head_nr) * g0.ua;
+    }
+    const StreamGeo g = g0;
 
     if (tid == 0) {
         S.abort = 0;
@@ -1419,77 +1432,92 @@ __global__ __launch_bounds__(SNT, 1) void decode_step_kernel(StepArgs a) {
         const int pu = stream_row_units(WT, D) - D / 256;
         const int hb = a.n_layers * g.LU;
         const int nh_w = g.nh > cw ? (g.nh - cw + NCW - 1) / NCW : 0;  // rows of this wavefront
-        const int nrw = min(head_nr, nh_w);                            // ... through the ring
-        const int nrb = (nrw + 3) / 4, ndb = (nh_w - nrw + 3) / 4;    // ring and direct batches
         // Lane r (< 4) of each batch takes the batch's row r: it stores that
         // logit and keeps a running (value, index, last NaN) over its rows;
         // the lanes merge once after the loop.
         float best_v = -INFINITY;
         int best_i = -1, nan_i = -1;
-        auto take = [&](const float (&res)[4], int r0, int n) {
-            const float v = lane == 0 ? res[0] : (lane == 1 ? res[1] : (lane == 2 ? res[2] : res[3]));
-            const int row = g.row0h + cw + NCW * (r0 + lane);
-            if (lane < n && row < a.vocab) {
-                st_c(&a.logits[row], v);
-                if (v != v) nan_i = max(nan_i, row);
-                else if (v > best_v || (v == best_v && row > best_i)) {
-                    best_v = v;
-                    best_i = row;
+        if constexpr (WT == WT_Q8_0) {
+            const int nrw = min(head_nr, nh_w);                            // ... through the ring
+            const int nrb = (nrw + 3) / 4, ndb = (nh_w - nrw + 3) / 4;    // ring and direct batches
+            auto take = [&](const float (&res)[4], int r0, int n) {
+                const float v = lane == 0 ? res[0] : (lane == 1 ? res[1] : (lane == 2 ? res[2] : res[3]));
+                const int row = g.row0h + cw + NCW * (r0 + lane);
+                if (lane < n && row < a.vocab) {
+                    st_c(&a.logits[row], v);
+                    if (v != v) nan_i = max(nan_i, row);
+                    else if (v > best_v || (v == best_v && row > best_i)) {
+                        best_v = v;
+                        best_i = row;
+                    }
                 }
-            }
-        };
-        // direct rows: batch b is rows r = nrw + 4b + q, read from the head
-        // matrix itself (rows past the wavefront's or the vocabulary's end
-        // read row 0; their results are dropped)
-        RowData dr[4];
-        auto issue_direct = [&](int b) {
-            const int blk = lane < KB ? lane : 0;
+            };
+            // direct rows: batch b is rows r = nrw + 4b + q, read from the head
+            // matrix itself (rows past the wavefront's or the vocabulary's end
+            // read row 0; their results are dropped)
+            RowData dr[4];
+            auto issue_direct = [&](int b) {
+                const int blk = lane < KB ? lane : 0;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int r = nrw + 4 * b + q;
-                int row = g.row0h + cw + NCW * r;
-                row = (r < nh_w && row < a.vocab) ? row : 0;
-                typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-                auto as_u4 = [](u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); };
-                if constexpr (WT == WT_Q8_0) {
+                for (int q = 0; q < 4; q++) {
+                    const int r = nrw + 4 * b + q;
+                    int row = g.row0h + cw + NCW * r;
+                    row = (r < nh_w && row < a.vocab) ? row : 0;
+                    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+                    auto as_u4 = [](u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); };
                     const gptr<const u32x4> p = (gptr<const u32x4>)(gl((const int8_t*)a.head.qs) + (size_t)row * D + 32 * blk);
                     dr[q].w0 = as_u4(p[0]);
                     dr[q].w1 = as_u4(p[1]);
-                } else {
-                    dr[q].w0 = as_u4(*(gptr<const u32x4>)(gl((const uint8_t*)a.head.qs) + (size_t)row * (D / 2) + 16 * blk));
-                    dr[q].w1 = dr[q].w0;
+                    dr[q].d = gl(a.head.scale)[(size_t)row * KB + blk];
                 }
-                dr[q].d = gl(a.head.scale)[(size_t)row * KB + blk];
-            }
-        };
-        auto direct_batch = [&](int b) {
-            float t[4];
+            };
+            auto direct_batch = [&](int b) {
+                float t[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) t[q] = row_math<WT>(dr[q], A, lane < KB);
-            wave_totals(t);
-            take(t, nrw + 4 * b, min(4, nh_w - nrw - 4 * b));
-        };
-        int db = 0;
-        if (ndb > 0) issue_direct(0);
+                for (int q = 0; q < 4; q++) t[q] = row_math<WT>(dr[q], A, lane < KB);
+                wave_totals(t);
+                take(t, nrw + 4 * b, min(4, nh_w - nrw - 4 * b));
+            };
+            int db = 0;
+            if (ndb > 0) issue_direct(0);
 #pragma unroll 1
-        for (int rb = 0; rb < nrb; rb++) {
-            const int r0 = 4 * rb;
-            const int n = min(4, nrw - r0);
-            float res[4];
-            if (!dot_batch(std::integral_constant<int, 4>{}, hb, g.ua, pu, r0, n, KB, A, res)) return fail();
-            consumed(hb + (cw + NCW * (r0 + n - 1) + 1) * g.ua);
-            take(res, r0, n);
-            // direct batches spread evenly over the ring batches, the next
-            // one's loads in flight meanwhile
-            if (db < ndb && db * nrb <= rb * ndb) {
+            for (int rb = 0; rb < nrb; rb++) {
+                const int r0 = 4 * rb;
+                const int n = min(4, nrw - r0);
+                float res[4];
+                if (!dot_batch(std::integral_constant<int, 4>{}, hb, g.ua, pu, r0, n, KB, A, res)) return fail();
+                consumed(hb + (cw + NCW * (r0 + n - 1) + 1) * g.ua);
+                take(res, r0, n);
+                // direct batches spread evenly over the ring batches, the next
+                // one's loads in flight meanwhile
+                if (db < ndb && db * nrb <= rb * ndb) {
+                    direct_batch(db);
+                    if (++db < ndb) issue_direct(db);
+                }
+            }
+#pragma unroll 1
+            while (db < ndb) {
                 direct_batch(db);
                 if (++db < ndb) issue_direct(db);
             }
-        }
+        } else {
 #pragma unroll 1
-        while (db < ndb) {
-            direct_batch(db);
-            if (++db < ndb) issue_direct(db);
+            for (int r0 = 0; r0 < nh_w; r0 += 4) {
+                const int n = min(4, nh_w - r0);
+                float res[4];
+                if (!dot_batch(std::integral_constant<int, 4>{}, hb, g.ua, pu, r0, n, KB, A, res)) return fail();
+                consumed(hb + (cw + NCW * (r0 + n - 1) + 1) * g.ua);
+                const float v = lane == 0 ? res[0] : (lane == 1 ? res[1] : (lane == 2 ? res[2] : res[3]));
+                const int row = g.row0h + cw + NCW * (r0 + lane);
+                if (lane < n && row < a.vocab) {
+                    st_c(&a.logits[row], v);
+                    if (v != v) nan_i = row;  // rows grow along the loop
+                    else if (v > best_v || (v == best_v && row > best_i)) {
+                        best_v = v;
+                        best_i = row;
+                    }
+                }
+            }
         }
         wave_arg(best_v, best_i, nan_i);
         consumed(g.total);
