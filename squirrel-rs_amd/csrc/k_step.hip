@@ -80,6 +80,8 @@ constexpr int RMAX = 2;            // residual rows a compute wavefront owns
 constexpr int head_ring_8ths(int wt) { return wt == WT_Q8_0 ? 4 : 8; }
 constexpr int XMAX = FMAX / 4 + FMAX / 32;  // exchange words gathered at once
 constexpr int WPT = (XMAX + CNT - 1) / CNT;  // ... per compute thread
+// during attention xw holds each wavefront's new K row and the tile slots' partials
+static_assert(NCW * HDIM + NCW * MAXG * (HDIM + 2) <= XMAX, "attention scratch exceeds xw");
 
 typedef float sq_v4f __attribute__((ext_vector_type(4)));
 typedef unsigned long long u64;
@@ -1105,6 +1107,133 @@ __global__ __launch_bounds__(SNT, 1) __attribute__((aligned(4096))) void decode_
                 const int gh = it / nchunks, chunk = it % nchunks;
                 const int t_begin = chunk * tpc, t_end = min(ntiles, t_begin + tpc);
                 const bool cur = t_end == ntiles;  // this chunk holds the new position
+                const int nt = t_end - t_begin;
+                if (nt > 1 && nt <= NCW) {
+                    // Tile slots: slot s takes tile t_begin + s for its share of
+                    // the group's query heads (NCW/NS wavefronts per slot), so the
+                    // chunk's tiles are in flight at once and each wavefront reads
+                    // one tile's K and V.  The slots' (o, m, l) meet in LDS and
+                    // wavefront j folds head j's in tile order: the same terms in
+                    // the same order as one wavefront walking the tiles.
+                    const int NS = nt == 2 ? 2 : NCW, WPS = NCW / NS, HPW = (GQ + WPS - 1) / WPS;
+                    const int slot = cw / WPS, j0 = (cw % WPS) * HPW, nh = min(HPW, GQ - j0);
+                    const int tile = t_begin + slot;
+                    float* part = (float*)(S.xw + NCW * HDIM);  // [NS][MAXG][HDIM + 2]
+                    if (nh > 0 && tile < t_end) {
+                        const int s0 = tile * TPOS;
+                        const bool last = tile == ntiles - 1;  // holds the new position
+                        sq_v4f kr[HDIM / 4];
+                        {
+                            const bool cached = s0 + lane < pos;
+                            const gptr<const sq_v4f> kp =
+                                (gptr<const sq_v4f>)(kc + (size_t)(cached ? s0 + lane : 0) * KVD + gh * HDIM);
+#pragma unroll
+                            for (int i = 0; i < HDIM / 4; i++) kr[i] = kp[i];
+                        }
+                        asm volatile("" ::: "memory");
+                        int t = tid;
+                        asm volatile("" : "+v"(t));
+                        const int d = t & 63;
+                        // q[lane] of this wavefront's heads, then the new K/V rows' element lane
+                        const u64* pw[MAXG + 2];
+                        u64 w[MAXG + 2];
+#pragma unroll
+                        for (int j = 0; j < MAXG; j++) pw[j] = j < nh ? X.q + (size_t)(gh * GQ + j0 + j) * HDIM + d : nullptr;
+                        pw[MAXG] = last ? X.k + gh * HDIM + d : nullptr;
+                        pw[MAXG + 1] = last ? X.v + gh * HDIM + d : nullptr;
+#pragma unroll
+                        for (int j = 0; j < MAXG + 2; j++) w[j] = pw[j] ? ld_c(pw[j]) : 0;
+                        if (!await_words(pw, w, Tin, C, &S.abort)) return fail();
+                        if (last) {
+                            unsigned* scr = S.xw + cw * HDIM;  // the new K row
+                            scr[lane] = (unsigned)w[MAXG];
+                            __builtin_amdgcn_wave_barrier();
+                            if (s0 + lane == pos) {
+#pragma unroll
+                                for (int i = 0; i < HDIM / 4; i++) kr[i] = *(const sq_v4f*)(scr + 4 * i);
+                            }
+                        }
+                        const float vn = __builtin_bit_cast(float, (unsigned)w[MAXG + 1]);
+                        if (it == wg) stamp(l, TS_ATT_Q);
+                        // scores = dot(q, k) * (1/sqrt(head_dim)) (attention.rs:52-55)
+                        float sc[MAXG];
+#pragma unroll
+                        for (int j = 0; j < MAXG; j++) {
+                            if (j >= nh) continue;
+                            const float qv = __builtin_bit_cast(float, (unsigned)w[j]);
+                            float dot = 0.0f;
+#pragma unroll
+                            for (int i = 0; i < HDIM / 4; i++) {
+                                dot += lane_value(qv, 4 * i + 0) * kr[i].x;
+                                dot += lane_value(qv, 4 * i + 1) * kr[i].y;
+                                dot += lane_value(qv, 4 * i + 2) * kr[i].z;
+                                dot += lane_value(qv, 4 * i + 3) * kr[i].w;
+                            }
+                            sc[j] = (s0 + lane < P) ? dot * scale : -INFINITY;
+                        }
+                        if (it == wg) stamp(l, TS_ATT_S);
+                        // V[s0 + sp][lane], row 0 standing in for positions
+                        // without a cached row (weight 0 below)
+                        float vv[TPOS];
+#pragma unroll
+                        for (int sp = 0; sp < TPOS; sp++) {
+                            const gptr<const float> vrow =
+                                vc + (size_t)(s0 + sp < pos ? s0 + sp : 0) * KVD + gh * HDIM;
+                            vv[sp] = vrow[lane];
+                        }
+#pragma unroll
+                        for (int j = 0; j < MAXG; j++) {
+                            if (j >= nh) continue;
+                            const float mt = wave_maximum(sc[j]);
+                            const float pr = (sc[j] == -INFINITY) ? 0.0f : expf(sc[j] - mt);
+                            const float lt = wave_total(pr);
+                            const float pm = s0 + lane == pos ? 0.0f : pr;
+                            float ot = 0.0f;
+#pragma unroll
+                            for (int k = 0; k < TPOS; k++) ot += lane_value(pm, k) * vv[k];
+                            if (s0 + TPOS > pos) ot += lane_value(pr, pos - s0) * vn;
+                            float* pp = part + (slot * MAXG + j0 + j) * (HDIM + 2);
+                            pp[lane] = ot;
+                            if (lane == 0) {
+                                pp[HDIM] = mt;
+                                pp[HDIM + 1] = lt;
+                            }
+                        }
+                    }
+                    if (!csync(S, gen, C)) return;
+                    if (cw < GQ) {
+                        const int h = gh * GQ + cw;
+                        float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
+                        for (int s = 0; s < nt; s++) {
+                            const float* pp = part + (s * MAXG + cw) * (HDIM + 2);
+                            const float mt = pp[HDIM], lt = pp[HDIM + 1], ot = pp[lane];
+                            // fold the tile into the chunk (the merge phase's arithmetic)
+                            if (mt != -INFINITY) {
+                                const float Mn = fmaxf(M, mt);
+                                const float es = (M == -INFINITY) ? 0.0f : expf(M - Mn);
+                                const float et = expf(mt - Mn);
+                                Lsum = Lsum * es + lt * et;
+                                O = O * es + ot * et;
+                                M = Mn;
+                            }
+                        }
+                        if (nchunks == 1) {
+                            quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, T, true,
+                                      tap_a ? (int*)tap_q(l, D) : nullptr, tap_a ? tap_d(l, D) : nullptr);
+                        } else {
+                            u64* pt = X.t + ((size_t)h * a.max_tiles + chunk) * (HDIM + 2);
+                            putf(pt + lane, O, T);
+                            if (lane == 0) {
+                                putf(pt + HDIM, M, T);
+                                putf(pt + HDIM + 1, Lsum, T);
+                            }
+                        }
+                    }
+                    if (it == wg) stamp(l, TS_ATT_PV);
+                    // the partials are read before a next item writes them
+                    if (it + G < items && !csync(S, gen, C)) return;
+                    continue;
+                }
                 if (cw >= GQ) continue;
                 const int h = gh * GQ + cw;
                 // the first tile's K rows are requested before the q words are
@@ -1228,53 +1357,111 @@ __global__ __launch_bounds__(SNT, 1) __attribute__((aligned(4096))) void decode_
                 // merge the chunks of each head, then quantize the row
                 const unsigned Tm = tag(l, PH_MERGE);
                 bool ok = true;
-                // from the last workgroup down: those are the last to get attention items
-                for (int h = (G - 1 - wg) * NCW + cw; h < a.n_heads && ok; h += G * NCW) {
-                    const int d = lane;
-                    float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
-                    const u64* ph = X.t + (size_t)h * a.max_tiles * (HDIM + 2);
-                    // (o[d], m, l) of the chunks t0 .. t0 + MT - 1, polled as one
-                    // batch and merged in chunk order
-                    auto merge_batch = [&](int t0, auto mt_c) -> bool {
-                        constexpr int MT = decltype(mt_c)::value;
-                        auto addr = [&](int j) -> const u64* {
-                            const int tt = t0 + j / 3;
-                            if (tt >= nchunks) return nullptr;
-                            const u64* pt = ph + (size_t)tt * (HDIM + 2);
-                            return j % 3 == 0 ? pt + d : pt + HDIM + (j % 3 - 1);
-                        };
-                        u64 w[3 * MT];
+                if (nchunks > 8) {
+                    // Many chunks: one workgroup per head (from the last one
+                    // down, as below).  Its wavefronts poll a round of up to
+                    // CPR chunks at once, wavefront cw chunks c0 + cw + NCW k,
+                    // into xw; wavefront 0 then folds them in chunk order.
+                    constexpr int CPR = 8 * NCW;
+                    static_assert(CPR * (HDIM + 2) <= XMAX, "merge round exceeds xw");
+                    float* part = (float*)S.xw;  // [chunk - c0][HDIM + 2]
+                    for (int h = G - 1 - wg; h < a.n_heads; h += G) {
+                        const u64* ph = X.t + (size_t)h * a.max_tiles * (HDIM + 2);
+                        float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
+                        for (int c0 = 0; c0 < nchunks; c0 += CPR) {
+                            auto addr = [&](int j) -> const u64* {
+                                const int c = c0 + cw + NCW * (j / 3);
+                                if (c >= nchunks) return nullptr;
+                                const u64* pt = ph + (size_t)c * (HDIM + 2);
+                                return j % 3 == 0 ? pt + lane : pt + HDIM + (j % 3 - 1);
+                            };
+                            u64 w[24];
 #pragma unroll
-                        for (int j = 0; j < 3 * MT; j++) w[j] = addr(j) ? ld_c(addr(j)) : 0;
-                        if (!await_words_at(addr, w, T, C, &S.abort)) return false;
+                            for (int j = 0; j < 24; j++) w[j] = addr(j) ? ld_c(addr(j)) : 0;
+                            const bool okw = await_words_at(addr, w, T, C, &S.abort);
+                            if (!__all(okw)) return fail();
 #pragma unroll
-                        for (int j2 = 0; j2 < MT; j2++) {
-                            if (t0 + j2 >= nchunks) continue;
-                            const float mt = __builtin_bit_cast(float, (unsigned)w[3 * j2 + 1]);
-                            if (mt == -INFINITY) continue;
-                            const float Mn = fmaxf(M, mt);
-                            const float es = (M == -INFINITY) ? 0.0f : expf(M - Mn);
-                            const float et = expf(mt - Mn);
-                            Lsum = Lsum * es + __builtin_bit_cast(float, (unsigned)w[3 * j2 + 2]) * et;
-                            O = O * es + __builtin_bit_cast(float, (unsigned)w[3 * j2]) * et;
-                            M = Mn;
+                            for (int k = 0; k < 8; k++) {
+                                const int c = c0 + cw + NCW * k;
+                                if (c >= nchunks) continue;
+                                float* pp = part + (c - c0) * (HDIM + 2);
+                                pp[lane] = __builtin_bit_cast(float, (unsigned)w[3 * k]);
+                                if (lane == 0) {
+                                    pp[HDIM] = __builtin_bit_cast(float, (unsigned)w[3 * k + 1]);
+                                    pp[HDIM + 1] = __builtin_bit_cast(float, (unsigned)w[3 * k + 2]);
+                                }
+                            }
+                            if (!csync(S, gen, C)) return;
+                            if (cw == 0) {
+                                const int n = min(CPR, nchunks - c0);
+                                for (int c = 0; c < n; c++) {
+                                    const float* pp = part + c * (HDIM + 2);
+                                    const float mt = pp[HDIM];
+                                    if (mt == -INFINITY) continue;
+                                    const float Mn = fmaxf(M, mt);
+                                    const float es = (M == -INFINITY) ? 0.0f : expf(M - Mn);
+                                    const float et = expf(mt - Mn);
+                                    Lsum = Lsum * es + pp[HDIM + 1] * et;
+                                    O = O * es + pp[lane] * et;
+                                    M = Mn;
+                                }
+                            }
+                            // the round's partials are folded before xw is written again
+                            if (!csync(S, gen, C)) return;
                         }
-                        return true;
-                    };
-                    // two chunks: one small batch; more: batches of eight
-                    if (nchunks <= 2) {
-                        ok = merge_batch(0, std::integral_constant<int, 2>{});
-                    } else {
-                        for (int t0 = 0; t0 < nchunks && ok; t0 += 8)
-                            ok = merge_batch(t0, std::integral_constant<int, 8>{});
+                        if (cw == 0)
+                            quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, Tm, true,
+                                      tap_a ? (int*)tap_q(l, D) : nullptr, tap_a ? tap_d(l, D) : nullptr);
                     }
-                    // lanes of one wavefront agree on ok (any failure aborts)
-                    if (__all(ok))
-                        quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, Tm, true,
-                                  tap_a ? (int*)tap_q(l, D) : nullptr, tap_a ? tap_d(l, D) : nullptr);
-                    else ok = false;
+                } else {
+                    // from the last workgroup down: those are the last to get attention items
+                    for (int h = (G - 1 - wg) * NCW + cw; h < a.n_heads && ok; h += G * NCW) {
+                        const int d = lane;
+                        float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
+                        const u64* ph = X.t + (size_t)h * a.max_tiles * (HDIM + 2);
+                        // (o[d], m, l) of the chunks t0 .. t0 + MT - 1, polled as one
+                        // batch and merged in chunk order
+                        auto merge_batch = [&](int t0, auto mt_c) -> bool {
+                            constexpr int MT = decltype(mt_c)::value;
+                            auto addr = [&](int j) -> const u64* {
+                                const int tt = t0 + j / 3;
+                                if (tt >= nchunks) return nullptr;
+                                const u64* pt = ph + (size_t)tt * (HDIM + 2);
+                                return j % 3 == 0 ? pt + d : pt + HDIM + (j % 3 - 1);
+                            };
+                            u64 w[3 * MT];
+#pragma unroll
+                            for (int j = 0; j < 3 * MT; j++) w[j] = addr(j) ? ld_c(addr(j)) : 0;
+                            if (!await_words_at(addr, w, T, C, &S.abort)) return false;
+#pragma unroll
+                            for (int j2 = 0; j2 < MT; j2++) {
+                                if (t0 + j2 >= nchunks) continue;
+                                const float mt = __builtin_bit_cast(float, (unsigned)w[3 * j2 + 1]);
+                                if (mt == -INFINITY) continue;
+                                const float Mn = fmaxf(M, mt);
+                                const float es = (M == -INFINITY) ? 0.0f : expf(M - Mn);
+                                const float et = expf(mt - Mn);
+                                Lsum = Lsum * es + __builtin_bit_cast(float, (unsigned)w[3 * j2 + 2]) * et;
+                                O = O * es + __builtin_bit_cast(float, (unsigned)w[3 * j2]) * et;
+                                M = Mn;
+                            }
+                            return true;
+                        };
+                        // two chunks: one small batch; more: batches of eight
+                        if (nchunks <= 2) {
+                            ok = merge_batch(0, std::integral_constant<int, 2>{});
+                        } else {
+                            for (int t0 = 0; t0 < nchunks && ok; t0 += 8)
+                                ok = merge_batch(t0, std::integral_constant<int, 8>{});
+                        }
+                        // lanes of one wavefront agree on ok (any failure aborts)
+                        if (__all(ok))
+                            quant_put(O / Lsum, lane, h * 2, X.a, X.a + QD / 4, Tm, true,
+                                      tap_a ? (int*)tap_q(l, D) : nullptr, tap_a ? tap_d(l, D) : nullptr);
+                        else ok = false;
+                    }
+                    if (!ok) return fail();
                 }
-                if (!ok) return fail();
                 stamp(l, TS_MERGE);
             }
         }
