@@ -840,12 +840,18 @@ enum TraceSlot : int {
 // neither runs the instance without them, whose code the compiler lays out
 // better (measured about 3.5% faster per token).
 //
+// WIDE: the attention paths of long contexts (items of several tiles spread
+// over the compute wavefronts, and a one-round merge of more than eight
+// chunks) are compiled in.  Either instance computes every position; the
+// host launches the wide one where those paths run, since the added code
+// makes the compiler's choices elsewhere cost 1-2% per token.
+//
 // Each instance starts on a 4 KB boundary.  The same machine code runs at
 // different speeds depending on where it starts modulo 4 KB (the Q4_0
 // instance between 1991 and 2087 tokens/s for start offsets 0x000-0xf00,
 // Q8_0 within 1%); aligned, an edit to one instance no longer moves the
 // others.
-template <int WT, bool INSTR>
+template <int WT, bool INSTR, bool WIDE>
 __global__ __launch_bounds__(SNT, 1) __attribute__((aligned(4096))) void decode_step_kernel(StepArgs a) {
     __shared__ StepShared S;
     // the wavefront index is uniform; readfirstlane lets the compiler keep
@@ -1108,7 +1114,7 @@ __global__ __launch_bounds__(SNT, 1) __attribute__((aligned(4096))) void decode_
                 const int t_begin = chunk * tpc, t_end = min(ntiles, t_begin + tpc);
                 const bool cur = t_end == ntiles;  // this chunk holds the new position
                 const int nt = t_end - t_begin;
-                if (nt > 1 && nt <= NCW) {
+                if (WIDE && nt > 1 && nt <= NCW) {
                     // Tile slots: slot s takes tile t_begin + s for its share of
                     // the group's query heads (NCW/NS wavefronts per slot), so the
                     // chunk's tiles are in flight at once and each wavefront reads
@@ -1357,7 +1363,7 @@ __global__ __launch_bounds__(SNT, 1) __attribute__((aligned(4096))) void decode_
                 // merge the chunks of each head, then quantize the row
                 const unsigned Tm = tag(l, PH_MERGE);
                 bool ok = true;
-                if (nchunks > 8) {
+                if (WIDE && nchunks > 8) {
                     // Many chunks: one workgroup per head (from the last one
                     // down, as below).  Its wavefronts poll a round of up to
                     // CPR chunks at once, wavefront cw chunks c0 + cw + NCW k,
@@ -1889,19 +1895,33 @@ int launch_build_stream(hipStream_t s, int wtype, const StepArgs& a, int grid, v
     return 0;
 }
 
-static int decode_step_resident(int wtype, bool instr, int* out);
+static int decode_step_resident(int wtype, bool instr, bool wide, int* out);
 
 // The step kernel instance for a weight type, with or without the
-// measurement and test outputs (null: not a step weight type).
-static const void* decode_step_function(int wtype, bool instr) {
-    if (wtype == WT_Q8_0)
-        return instr ? (const void*)decode_step_kernel<WT_Q8_0, true> : (const void*)decode_step_kernel<WT_Q8_0, false>;
-    if (wtype == WT_Q4_0)
-        return instr ? (const void*)decode_step_kernel<WT_Q4_0, true> : (const void*)decode_step_kernel<WT_Q4_0, false>;
+// measurement and test outputs and the long-context attention paths (null:
+// not a step weight type).
+template <int WT>
+static const void* decode_step_function_t(bool instr, bool wide) {
+    if (instr)
+        return wide ? (const void*)decode_step_kernel<WT, true, true> : (const void*)decode_step_kernel<WT, true, false>;
+    return wide ? (const void*)decode_step_kernel<WT, false, true> : (const void*)decode_step_kernel<WT, false, false>;
+}
+static const void* decode_step_function(int wtype, bool instr, bool wide) {
+    if (wtype == WT_Q8_0) return decode_step_function_t<WT_Q8_0>(instr, wide);
+    if (wtype == WT_Q4_0) return decode_step_function_t<WT_Q4_0>(instr, wide);
     return nullptr;
 }
 
-int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid) {
+// True when a step at position pos has attention items of several tiles or
+// more than eight chunks per head (the kernel's own item geometry).
+static bool decode_step_wide(int pos, int n_kv_heads, int grid) {
+    const int ntiles = (pos + TPOS) / TPOS;
+    const int tpc = (ntiles * n_kv_heads + grid - 1) / grid;
+    const int nchunks = (ntiles + tpc - 1) / tpc;
+    return tpc > 1 || nchunks > 8;
+}
+
+int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid, int pos) {
     if (!decode_step_fits(a.dim, a.ffn, a.n_heads, a.n_kv_heads, grid))
         return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: shape not supported (dim <= 2048, ffn <= 8192, "
                                              "multiples of 256, GQA group <= 4)");
@@ -1917,36 +1937,31 @@ int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid) {
     if (wtype != WT_Q8_0 && wtype != WT_Q4_0)
         return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: Q8_0 and Q4_0 weights only");
     const bool instr = a.taps != 0 || a.trace != nullptr;
+    const bool wide = decode_step_wide(pos, a.n_kv_heads, grid);
     int resident = 0;
-    if (int st = decode_step_resident(wtype, instr, &resident)) return st;
+    if (int st = decode_step_resident(wtype, instr, wide, &resident)) return st;
     if (grid > resident)
         return set_error(SQ_ERR_HIP, "decode step launch: a grid of " + std::to_string(grid) +
                                          " workgroups cannot be resident at once on this device (at most " +
                                          std::to_string(resident) + ")");
-    if (wtype == WT_Q8_0 && instr)
-        hipLaunchKernelGGL((decode_step_kernel<WT_Q8_0, true>), dim3(grid), dim3(SNT), 0, s, a);
-    else if (wtype == WT_Q8_0)
-        hipLaunchKernelGGL((decode_step_kernel<WT_Q8_0, false>), dim3(grid), dim3(SNT), 0, s, a);
-    else if (instr)
-        hipLaunchKernelGGL((decode_step_kernel<WT_Q4_0, true>), dim3(grid), dim3(SNT), 0, s, a);
-    else
-        hipLaunchKernelGGL((decode_step_kernel<WT_Q4_0, false>), dim3(grid), dim3(SNT), 0, s, a);
-    const hipError_t e = hipGetLastError();
+    const void* f = decode_step_function(wtype, instr, wide);
+    void* args[] = {(void*)&a};
+    const hipError_t e = hipLaunchKernel(f, dim3(grid), dim3(SNT), args, 0, s);
     if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("decode step launch: ") + hipGetErrorString(e));
     return 0;
 }
 
 // Workgroups of a step kernel instance the current device holds at once (per
 // CU times CUs), looked up once per device.
-static int decode_step_resident(int wtype, bool instr, int* out) {
-    static int cached[2][2][64] = {};
+static int decode_step_resident(int wtype, bool instr, bool wide, int* out) {
+    static int cached[2][2][2][64] = {};
     int dev = 0;
     SQ_HIP_CHECK(hipGetDevice(&dev));
-    int& slot = cached[wtype == WT_Q4_0 ? 1 : 0][instr ? 1 : 0][dev & 63];
+    int& slot = cached[wtype == WT_Q4_0 ? 1 : 0][instr ? 1 : 0][wide ? 1 : 0][dev & 63];
     if (slot == 0) {
         int cus = 0, per_cu = 0;
         SQ_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        const void* f = decode_step_function(wtype, instr);
+        const void* f = decode_step_function(wtype, instr, wide);
         if (!f) return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: Q8_0 and Q4_0 weights only");
         SQ_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, SNT, 0));
         slot = per_cu * cus;
@@ -1959,9 +1974,10 @@ int decode_step_max_grid(int wtype, int* grid) {
     int dev = 0, cus = 0, resident = 0;
     SQ_HIP_CHECK(hipGetDevice(&dev));
     SQ_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    // both instances (with and without the measurement outputs) must fit
-    for (int instr = 0; instr < 2; instr++) {
-        if (int st = decode_step_resident(wtype, instr != 0, &resident)) return st;
+    // every instance (with and without the measurement outputs and the
+    // long-context paths) must fit
+    for (int v = 0; v < 4; v++) {
+        if (int st = decode_step_resident(wtype, (v & 1) != 0, (v & 2) != 0, &resident)) return st;
         if (resident < cus) return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step does not fit on a CU");
     }
     *grid = cus;

@@ -210,8 +210,10 @@ size_t decode_stream_stride(int wtype, int n_layers, int dim, int ffn, int n_hea
 // Fills dst (grid * stride units) with the per-CU weight streams of the
 // layers, head and geometry in `a` (a.stream_stride must be the stride).
 int launch_build_stream(hipStream_t s, int wtype, const StepArgs& a, int grid, void* dst);
-// Launch of one decode step over `grid` workgroups (one per CU).
-int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid);
+// Launch of one decode step over `grid` workgroups (one per CU).  pos, the
+// position the step decodes as the host counts it, picks the kernel instance
+// (any instance computes every position).
+int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid, int pos);
 // Workgroups for the decode step on the current device (one per CU).
 int decode_step_max_grid(int wtype, int* grid);
 

@@ -559,7 +559,7 @@ int build_decode_step(sq_ctx* c) {
 }
 
 int run_decode_step(sq_ctx* c) {
-    if (c->persist) return launch_decode_step(c->stream, c->m->wtype, c->step, c->step_grid);
+    if (c->persist) return launch_decode_step(c->stream, c->m->wtype, c->step, c->step_grid, (int)c->seq_len);
     if (c->graph) {
         SQ_HIP_CHECK(hipGraphLaunch(c->graph, c->stream));
         return 0;

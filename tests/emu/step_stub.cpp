@@ -13,7 +13,7 @@ size_t exchange_words(int, int, int, int, int, int) { return 0; }
 int launch_build_stream(hipStream_t, int, const StepArgs&, int, void*) {
     return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step is not emulated");
 }
-int launch_decode_step(hipStream_t, int, const StepArgs&, int) {
+int launch_decode_step(hipStream_t, int, const StepArgs&, int, int) {
     return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step is not emulated");
 }
 int decode_step_max_grid(int, int* grid) {
