@@ -1937,7 +1937,10 @@ int launch_decode_step(hipStream_t s, int wtype, const StepArgs& a, int grid, in
     if (wtype != WT_Q8_0 && wtype != WT_Q4_0)
         return set_error(SQ_ERR_UNSUPPORTED, "persistent decode step: Q8_0 and Q4_0 weights only");
     const bool instr = a.taps != 0 || a.trace != nullptr;
-    const bool wide = decode_step_wide(pos, a.n_kv_heads, grid);
+    // SQUIRREL_STEP_WIDE=1 / =0 pins the instance (a test and measurement
+    // aid: both compute every position, bit for bit alike)
+    const char* pin = getenv("SQUIRREL_STEP_WIDE");
+    const bool wide = pin && (pin[0] == '0' || pin[0] == '1') ? pin[0] == '1' : decode_step_wide(pos, a.n_kv_heads, grid);
     int resident = 0;
     if (int st = decode_step_resident(wtype, instr, wide, &resident)) return st;
     if (grid > resident)

@@ -301,6 +301,33 @@ def test_persistent_deterministic_across_resets(tiny_gguf):
     assert np.array_equal(l1, l2) and np.array_equal(l1, l3)
 
 
+@pytest.mark.parametrize("variant,grid,n_prompt", [
+    ("g4", "64", 2100),   # two-tile items in two slots of two heads, then a one-round merge of 17 chunks
+    ("g2", "32", 1050),   # two-tile items in two slots of one head, then a one-round merge of 9 chunks
+    ("g2", None, 600),    # one-tile items, then a one-round merge of 10 chunks
+])
+def test_step_wide_and_narrow_instances_agree(tiny_gguf, variant, grid, n_prompt, monkeypatch):
+    """The decode step is built with and without the long-context attention
+    forms (tile slots, the one-round merge); the host picks the first where
+    they run.  Pinned to one or the other (SQUIRREL_STEP_WIDE), both compute
+    the same logits bit for bit: the slots and the one-round merge fold the
+    same terms in the same order as the one-wavefront walk and the batched
+    merge."""
+    if grid:
+        monkeypatch.setenv("SQUIRREL_STEP_GRID", grid)
+    path = tiny_gguf("Q8_0", variant)
+    seq = teacher_seq(1000, n_prompt=n_prompt, n_decode=6, seed=29)
+    runs = {}
+    for pin in ("1", "0"):
+        monkeypatch.setenv("SQUIRREL_STEP_WIDE", pin)
+        got, toks, (m, c, _) = run_gpu(path, seq, max_pos=n_prompt + 16, taps=False)
+        assert c.persistent
+        runs[pin] = (got, toks)
+    assert runs["1"][1] == runs["0"][1]
+    for step, (a, b) in enumerate(zip(runs["1"][0], runs["0"][0])):
+        assert np.array_equal(a, b), f"step {step}: the two instances differ"
+
+
 @pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
 def test_step_instances_agree(tiny_gguf, wtype):
     """The persistent step is built twice: with the measurement and test
