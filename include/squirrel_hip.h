@@ -282,8 +282,9 @@ int sq_ctx_prefill_phases(sq_ctx* c, const uint32_t* ids, size_t n, double* ms);
  * (measurement and test aid, no reference counterpart): out[0] all, [1] those
  * that split K over workgroups, [2] those on the full-rate kernel's 128 x 128
  * tiles, [3] the largest split count, [4] those on the full-rate kernel's
- * 128 x 64 tiles (out holds 5 values).  out may be null; reset != 0 zeroes the
- * counters afterwards. */
+ * 128 x 64 tiles, [5] those on the few-rows kernel (32 x 32 tiles, inputs of
+ * at most 32 rows) (out holds 6 values).  out may be null; reset != 0 zeroes
+ * the counters afterwards. */
 int sq_gemm_counters(int reset, uint64_t* out);
 
 #ifdef __cplusplus

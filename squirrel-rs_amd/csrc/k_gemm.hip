@@ -614,6 +614,131 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
     *o = accumulate ? *o + v : v;
 }
 
+// ---- few activation rows: the weights streamed once --------------------------
+// A prompt of a few dozen rows (the short prompts of a generation) makes the
+// matmul a weight stream with little arithmetic per byte.  The 64 x 64
+// kernel leaves most of its tile empty there, and on narrow matrices splits
+// K over workgroups and sums the partials in a second launch.  Here a
+// workgroup takes 32 weight rows and 32 activation rows: one
+// v_mfma_i32_32x32x32_i8 per block (lane l supplies 16 bytes of row l % 32,
+// half l / 32 of the block; activations as operand A, weights as operand B)
+// and one v_mfma_f32_32x32x8f16 for the scale products sa * sw (lanes 0-31
+// hold the row's and the column's scale in k-slot 0, the others zeros).  Its
+// RW_NW wavefronts take consecutive ranges of K, each with two batches of
+// RW_NB blocks of loads in flight (branch-free: blocks past a range read a
+// clamped address and get zero scales), and sum their partial tiles through
+// LDS in wavefront order.  The per-block combine is that of the other
+// kernels: fma(f32(isum), sa * sw, acc) (dot_prod.rs:189-252).
+constexpr int RW_NW = 8;  // wavefronts per workgroup
+constexpr int RW_NB = 4;  // blocks per load batch
+
+typedef unsigned short rw_scales __attribute__((ext_vector_type(RW_NB)));
+struct RwBatch {
+    sq_v4i w[RW_NB];      // Q8_0: 16 bytes of the block; Q4_0: the packed block
+    sq_v4i a[RW_NB];
+    rw_scales sw, sa;     // the batch's f16 block scales of this lane's weight row and activation row
+};
+
+template <int WT>
+__global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const int8_t* __restrict__ aq,
+                                                               const uint16_t* __restrict__ ad, int m_rows,
+                                                               float* __restrict__ out, int ldo, int accumulate,
+                                                               int per) {
+    __shared__ float red[RW_NW][16][64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int K = w.k, KB = K >> 5;
+    const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+    const int fr = lane & 31, fh = lane >> 5;
+    // this wavefront's blocks [kbw, kend), per (a multiple of 2 RW_NB) per wavefront
+    const int kbw = wave * per, kend = min(KB, kbw + per);
+    const int nb = per / RW_NB;
+    const size_t wrow = (size_t)min(n0 + fr, w.rows - 1), arow = (size_t)min(m0 + fr, m_rows - 1);
+    const bool wvalid = n0 + fr < w.rows;
+
+    auto load = [&](RwBatch& B, int kb) {
+        const int kc = min(kb, KB - RW_NB);  // KB is a multiple of RW_NB
+#pragma unroll
+        for (int j = 0; j < RW_NB; j++) {
+            if constexpr (WT == WT_Q8_0)
+                B.w[j] = *(const sq_v4i*)((const int8_t*)w.qs + wrow * K + (kc + j) * 32 + 16 * fh);
+            else
+                B.w[j] = *(const sq_v4i*)((const uint8_t*)w.qs + wrow * (K / 2) + (kc + j) * 16);
+            B.a[j] = *(const sq_v4i*)(aq + arow * K + (kc + j) * 32 + 16 * fh);
+        }
+        B.sw = *(const rw_scales*)(w.scale + wrow * KB + kc);
+        B.sa = *(const rw_scales*)(ad + arow * KB + kc);
+    };
+    m8_v16f acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    const m8_v16i izero = {};
+    const m8_v16f fzero = {};
+    auto compute = [&](const RwBatch& B, int kb) {
+#pragma unroll
+        for (int j = 0; j < RW_NB; j++) {
+            sq_v4i wf = B.w[j];
+            if constexpr (WT == WT_Q4_0) {
+                // byte t holds element t (low nibble) and t + 16 (high nibble):
+                // half fh of the block is one nibble of every byte, as q - 8
+                // in a signed byte ((q | 0x80) - 8 stays within the byte, and
+                // xor 0x80 restores the sign)
+                const int sh = 4 * fh;
+                wf.x = (int)(((((unsigned)wf.x >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+                wf.y = (int)(((((unsigned)wf.y >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+                wf.z = (int)(((((unsigned)wf.z >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+                wf.w = (int)(((((unsigned)wf.w >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+            }
+            // blocks past the range fold nothing: both scales zero (an
+            // activation scale may be inf, and inf * 0 would not be).  Lane
+            // l % 32 carries activation row l % 32 in sa and weight row
+            // l % 32 in sw, so a weight row past the matrix zeroes only sw.
+            // (selects, not branches: a branch here lets the compiler move
+            // every block's combine after all the matrix instructions)
+            const bool inb = kb + j < kend && fh == 0;
+            const uint16_t sav = inb ? (uint16_t)B.sa[j] : (uint16_t)0, swv = inb && wvalid ? (uint16_t)B.sw[j] : (uint16_t)0;
+            const _Float16 h0 = 0;
+            const mq_v4h sa = {__builtin_bit_cast(_Float16, sav), h0, h0, h0};
+            const mq_v4h sw = {__builtin_bit_cast(_Float16, swv), h0, h0, h0};
+            const m8_v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(B.a[j], wf, izero, 0, 0, 0);
+            const m8_v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sw, fzero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[r] = fmaf((float)d[r], sc[r], acc[r]);
+            // one block's products live at a time: left to itself the
+            // scheduler issues every block's matrix instructions first and
+            // spills their results
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    RwBatch B0, B1;
+    load(B0, kbw);
+    load(B1, kbw + RW_NB);
+    for (int b = 0; b + 2 < nb; b += 2) {
+        compute(B0, kbw + b * RW_NB);
+        load(B0, kbw + (b + 2) * RW_NB);
+        compute(B1, kbw + (b + 1) * RW_NB);
+        load(B1, kbw + (b + 3) * RW_NB);
+    }
+    compute(B0, kbw + (nb - 2) * RW_NB);
+    compute(B1, kbw + (nb - 1) * RW_NB);
+
+    // partial tiles summed in wavefront order; element r of lane l is row
+    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
+#pragma unroll
+    for (int r = 0; r < 16; r++) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    for (int e = tid; e < 16 * 64; e += RW_NW * 64) {
+        const int r = e >> 6, l = e & 63;
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RW_NW; q++) v += red[q][r][l];
+        const int mm = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), nn = n0 + (l & 31);
+        if (mm < m_rows && nn < w.rows) {
+            float* o = out + (size_t)mm * ldo + nn;
+            *o = accumulate ? *o + v : v;
+        }
+    }
+}
+
 // Compute units of the current device (the grid-size rules below are in
 // workgroups per CU).
 int device_cus() {
@@ -632,10 +757,12 @@ int device_cus() {
 // full-rate 128 x 128 tiles, the largest split count, full-rate 128 x 64
 // tiles.
 std::atomic<uint64_t> g_launches{0}, g_split_launches{0}, g_tile128_launches{0}, g_max_splits{0},
-    g_tile128x64_launches{0};
-// bn: 0 for the 64 x 64 kernel, else the full-rate kernel's tile columns (64 or 128)
+    g_tile128x64_launches{0}, g_rows_launches{0};
+// bn: 0 for the 64 x 64 kernel, 32 for the few-rows kernel, else the
+// full-rate kernel's tile columns (64 or 128)
 void count_launch(int splits, int bn) {
     g_launches++;
+    if (bn == 32) g_rows_launches++;
     if (splits > 1) g_split_launches++;
     if (bn == 128) g_tile128_launches++;
     if (bn == 64) g_tile128x64_launches++;
@@ -723,24 +850,51 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
     return 0;
 }
 
+// The few-rows kernel: grid (column tiles of 32, row tiles of 32), K in
+// blocks of 32 with KB a multiple of RW_NB.
+template <int WT>
+int run_rows(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
+             bool acc) {
+    const int KB = w.k / 32;
+    const int per = ((KB + RW_NW - 1) / RW_NW + 2 * RW_NB - 1) / (2 * RW_NB) * (2 * RW_NB);
+    count_launch(1, 32);
+    hipLaunchKernelGGL(gemm_rows_kernel<WT>, dim3((w.rows + 31) / 32, (m + 31) / 32), dim3(RW_NW * 64), 0, s, w, aq,
+                       ad, m, out, ldo, acc ? 1 : 0, per);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+    return 0;
+}
+
 // SQUIRREL_GEMM_TILE pins the prefill matmul's kernel (a test and
 // measurement aid): "64" the 64 x 64 kernel, "128x64" and "128" the
-// full-rate kernel on 128 x 64 or 128 x 128 tiles.  Unset, the largest
-// full-rate tiling whose grid fills the device is taken.
-enum : int { TILE_AUTO = 0, TILE_64 = 1, TILE_128X64 = 2, TILE_128 = 3 };
+// full-rate kernel on 128 x 64 or 128 x 128 tiles, "rows" the few-rows
+// kernel.  Unset, inputs of at most 32 rows take the few-rows kernel, and
+// larger ones the largest full-rate tiling whose grid fills the device.
+enum : int { TILE_AUTO = 0, TILE_64 = 1, TILE_128X64 = 2, TILE_128 = 3, TILE_ROWS = 4 };
 int gemm_tile_override() {
     const char* e = getenv("SQUIRREL_GEMM_TILE");
     if (!e) return TILE_AUTO;
     if (!strcmp(e, "64")) return TILE_64;
     if (!strcmp(e, "128x64")) return TILE_128X64;
     if (!strcmp(e, "128")) return TILE_128;
+    if (!strcmp(e, "rows")) return TILE_ROWS;
     return TILE_AUTO;
+}
+
+// Inputs the few-rows kernel takes unless a tiling is pinned: up to 32 rows
+// and K up to 4096.  (At K = 8192 its 32-row tiles leave the FFN down
+// projection 64 workgroups, and the 64 x 64 kernel's K split measured
+// 14.9 against 25.5 us for a 32-token prompt.)
+bool rows_kernel_fits(int m, int k) {
+    return m <= 32 && k <= 4096 && (k / 32) % RW_NB == 0 && gemm_tile_override() == TILE_AUTO;
 }
 
 template <int WT>
 int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
                 bool acc, float* ws, size_t ws_floats) {
     const int tile = gemm_tile_override();
+    if ((tile == TILE_ROWS && (w.k / 32) % RW_NB == 0) || rows_kernel_fits(m, w.k))
+        return run_rows<WT>(s, w, aq, ad, m, out, ldo, acc);
     if (tile == TILE_128 || (tile == TILE_AUTO && m >= 128)) {
         const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128);
         if (st != 1) return st;
@@ -786,6 +940,7 @@ void gemm_counters(bool reset, uint64_t* out) {
         out[2] = g_tile128_launches.load();
         out[3] = g_max_splits.load();
         out[4] = g_tile128x64_launches.load();
+        out[5] = g_rows_launches.load();
     }
     if (reset) {
         g_launches = 0;
@@ -793,6 +948,7 @@ void gemm_counters(bool reset, uint64_t* out) {
         g_tile128_launches = 0;
         g_max_splits = 0;
         g_tile128x64_launches = 0;
+        g_rows_launches = 0;
     }
 }
 
@@ -807,11 +963,13 @@ int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_
         // (without a workspace for a K split, inputs below one 64-row tile
         // stay on the VALU kernel, which spreads the weights over more workgroups)
         case WT_Q8_0:
-            if (a8 && (m >= MQ_T || ws != nullptr)) return run_integer<WT_Q8_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
+            if (a8 && (m >= MQ_T || ws != nullptr || rows_kernel_fits(m, w.k)))
+                return run_integer<WT_Q8_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
             return a8 ? dispatch<WT_Q8_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q8_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_Q4_0:
-            if (a8 && (m >= MQ_T || ws != nullptr)) return run_integer<WT_Q4_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
+            if (a8 && (m >= MQ_T || ws != nullptr || rows_kernel_fits(m, w.k)))
+                return run_integer<WT_Q4_0>(s, v, aq, ad, m, out, ldo, accumulate, ws, ws_floats);
             return a8 ? dispatch<WT_Q4_0, true>(s, v, aq, ad, x, m, out, ldo, accumulate)
                       : dispatch<WT_Q4_0, false>(s, v, aq, ad, x, m, out, ldo, accumulate);
         case WT_BF16:

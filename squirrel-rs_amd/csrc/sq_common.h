@@ -62,6 +62,7 @@ struct MatView {
     int rows;
     int k;
     int wtype;
+    int pad = 0;  // the struct's tail, zero rather than whatever the stack held
 };
 
 inline MatView view(const DevMatrix& m) { return MatView{m.qs, m.scale, m.rows, m.k, m.wtype}; }

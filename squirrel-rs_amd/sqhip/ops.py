@@ -175,10 +175,10 @@ def softmax(a: DeviceArray, out: DeviceArray) -> None:
 
 def gemm_counters(reset: bool = False) -> dict:
     """Matrix-core matmul launches since the last reset (sq_gemm_counters)."""
-    out = np.zeros(5, np.uint64)
+    out = np.zeros(6, np.uint64)
     check(lib().sq_gemm_counters(1 if reset else 0, out.ctypes.data))
     return {"launches": int(out[0]), "split_launches": int(out[1]), "tile128_launches": int(out[2]),
-            "max_splits": int(out[3]), "tile128x64_launches": int(out[4])}
+            "max_splits": int(out[3]), "tile128x64_launches": int(out[4]), "rows_launches": int(out[5])}
 
 
 def log_softmax_at(logits: DeviceArray, idx: int) -> float:

@@ -244,7 +244,8 @@ def test_long_prefill_unsplit_matrix_core_tiles(tiny_gguf, wtype):
     """A 2048-token prompt gives every prefill matmul of the g4 model at least
     256 output tiles (8 x 32 for the o and down projections), so they run on
     the matrix cores without the K split, accumulating the residual in place;
-    shorter prompts take the split path."""
+    a prompt of at most 32 tokens takes the few-rows kernel (no split
+    either)."""
     from sqhip import ops
     path = tiny_gguf(wtype, "g4")
     seq = teacher_seq(2048, n_prompt=2048, n_decode=2, seed=17)
@@ -257,7 +258,7 @@ def test_long_prefill_unsplit_matrix_core_tiles(tiny_gguf, wtype):
     c.reset_cache()
     c.forward(np.asarray(seq[0][:13]))
     n = ops.gemm_counters(reset=True)
-    assert n["launches"] == 8 and n["split_launches"] == 8 and n["max_splits"] > 1, n  # a 13-token prompt splits
+    assert n["launches"] == 8 and n["rows_launches"] == 8 and n["split_launches"] == 0, n  # a 13-token prompt
     for g, t in zip(got, toks):
         assert t == O.greedy(g)
 
@@ -672,4 +673,4 @@ def test_full_width_prefill_2048(model_dir):
                max_pos=2064)
     n = ops.gemm_counters(reset=True)
     assert n == {"launches": 8, "split_launches": 0, "tile128_launches": 2, "max_splits": 1,
-                 "tile128x64_launches": 6}, n
+                 "tile128x64_launches": 6, "rows_launches": 0}, n

@@ -187,7 +187,62 @@ def test_matmul_tiles_agree(wtype, monkeypatch):
     assert np.all(err <= 4e-6 * term_mag(x[rows], wf) + 1e-6)
 
 
-@pytest.mark.parametrize("tile", ["64", "128x64", "128"])
+@pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("m,k,n,pin", [
+    (2, 2048, 2048, None), (13, 2048, 3072, None), (32, 8192, 2048, "rows"), (29, 128, 7, None),
+    (7, 512, 1000, None), (45, 2048, 512, "rows"), (200, 1024, 96, "rows"),
+])
+def test_matmul_rows_kernel_matches_oracle(wtype, m, k, n, pin, monkeypatch):
+    """The few-rows prefill matmul (inputs of at most 32 rows, or pinned with
+    SQUIRREL_GEMM_TILE=rows): 32 x 32 tiles, K split over the workgroup's
+    wavefronts and summed in wavefront order.  Ragged rows and columns, K of
+    one load batch (128), and several row tiles when pinned; every output
+    within 4e-6 of its sum of |terms| of the oracle (matmul.rs:133-171), and
+    added in place with accumulate."""
+    if pin:
+        monkeypatch.setenv("SQUIRREL_GEMM_TILE", pin)
+    w, _ = quant_weights(wtype, n, k, seed=101 + m)
+    x = (rng(m).standard_normal((m, k)) * 1.5).astype(np.float32)
+    W = ops.Weight(wtype, w, n, k)
+    out = DeviceArray((m, n))
+    ops.gemm_counters(reset=True)
+    ops.linear(DeviceArray.from_numpy(x), W, out)
+    c = ops.gemm_counters(reset=True)
+    assert c["launches"] == 1 and c["rows_launches"] == 1 and c["split_launches"] == 0, c
+    got = out.numpy().astype(np.float64)
+    rows = np.arange(0, m, max(1, m // 9))
+    want = O.linear(x[rows], wtype, w, n, O.W8A8)
+    wf = np.stack([O.dequantize(wtype, w[i], k) for i in range(n)])
+    err = np.abs(got[rows] - want)
+    assert np.all(err <= 4e-6 * term_mag(x[rows], wf) + 1e-6), float(err.max())
+
+
+def test_matmul_rows_kernel_inf_activation_scale():
+    """An activation block of f32::MAX/2 has a Q8_0 scale that overflows
+    binary16 to inf (dot_prod.rs:629-654): that row's outputs are +-inf or
+    NaN, as the oracle's, element for element, and the other rows match the
+    oracle within the usual bound."""
+    m, k, n = 4, 256, 64
+    w, _ = quant_weights(O.Q8_0, n, k, seed=5)
+    x = (rng(6).standard_normal((m, k))).astype(np.float32)
+    x[1, 224:256] = np.float32(np.finfo(np.float32).max / 2)   # the last block of row 1
+    W = ops.Weight(O.Q8_0, w, n, k)
+    out = DeviceArray((m, n))
+    ops.gemm_counters(reset=True)
+    ops.linear(DeviceArray.from_numpy(x), W, out)
+    assert ops.gemm_counters(reset=True)["rows_launches"] == 1
+    got = out.numpy().astype(np.float64)
+    want = O.linear(x, O.Q8_0, w, n, O.W8A8)
+    assert not np.all(np.isfinite(want[1]))
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~fin & ~np.isnan(want)], want[~fin & ~np.isnan(want)])
+    wf = np.stack([O.dequantize(O.Q8_0, w[i], k) for i in range(n)])
+    mag = term_mag(x, wf)
+    assert np.all(np.abs(got[fin] - want[fin]) <= 4e-6 * mag[fin] + 1e-6)
+
+
+@pytest.mark.parametrize("tile", ["64", "128x64", "128", "rows"])
 def test_matmul_subnormal_activation_scales(tile, monkeypatch):
     """Activation rows of magnitude about 1e-4 have Q8_0 block scales below
     binary16's smallest normal (6.1e-5): the matrix-core kernels form the
@@ -208,7 +263,8 @@ def test_matmul_subnormal_activation_scales(tile, monkeypatch):
     ops.linear(DeviceArray.from_numpy(x), W, out)
     c = ops.gemm_counters(reset=True)
     assert c["tile128_launches"] == (1 if tile == "128" else 0) and \
-        c["tile128x64_launches"] == (1 if tile == "128x64" else 0), c
+        c["tile128x64_launches"] == (1 if tile == "128x64" else 0) and \
+        c["rows_launches"] == (1 if tile == "rows" else 0), c
     got = out.numpy().astype(np.float64)
     rows = np.arange(0, m, 13)
     want = O.linear(x[rows], O.Q8_0, w, n, O.W8A8)
