@@ -619,75 +619,82 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
 // matmul a weight stream with little arithmetic per byte.  The 64 x 64
 // kernel leaves most of its tile empty there, and on narrow matrices splits
 // K over workgroups and sums the partials in a second launch.  Here a
-// workgroup takes 32 weight rows and 32 activation rows: one
-// v_mfma_i32_32x32x32_i8 per block (lane l supplies 16 bytes of row l % 32,
-// half l / 32 of the block; activations as operand A, weights as operand B)
-// and one v_mfma_f32_32x32x8f16 for the scale products sa * sw (lanes 0-31
-// hold the row's and the column's scale in k-slot 0, the others zeros).  Its
-// RW_NW wavefronts take consecutive ranges of K, each with two batches of
-// RW_NB blocks of loads in flight (branch-free: blocks past a range read a
-// clamped address and get zero scales), and sum their partial tiles through
-// LDS in wavefront order.  The per-block combine is that of the other
-// kernels: fma(f32(isum), sa * sw, acc) (dot_prod.rs:189-252).
+// workgroup takes 32 activation rows and NT tiles of 32 weight rows: one
+// v_mfma_i32_32x32x32_i8 per block and tile (lane l supplies 16 bytes of row
+// l % 32, half l / 32 of the block; activations as operand A, weights as
+// operand B) and one v_mfma_f32_32x32x8f16 for the scale products sa * sw
+// (lanes 0-31 hold the row's and the column's scale in k-slot 0, the others
+// zeros).  Its RW_NW wavefronts take consecutive ranges of the workgroup's
+// K, each with two batches of RW_NB blocks of loads in flight (branch-free:
+// blocks past a range read a clamped address and get zero scales), and sum
+// their partial tiles through LDS in wavefront order.  A long K on a narrow
+// matrix is also split over workgroups (blockIdx.z), whose partial tiles
+// split_sum_kernel adds in split order.  The per-block combine is that of
+// the other kernels: fma(f32(isum), sa * sw, acc) (dot_prod.rs:189-252).
 constexpr int RW_NW = 8;  // wavefronts per workgroup
-constexpr int RW_NB = 4;  // blocks per load batch
+constexpr int RW_NB = 4;  // blocks per load batch with one column tile (two with two)
 
-typedef unsigned short rw_scales __attribute__((ext_vector_type(RW_NB)));
+template <int NT, int NB>
 struct RwBatch {
-    sq_v4i w[RW_NB];      // Q8_0: 16 bytes of the block; Q4_0: the packed block
-    sq_v4i a[RW_NB];
-    rw_scales sw, sa;     // the batch's f16 block scales of this lane's weight row and activation row
+    typedef unsigned short scales __attribute__((ext_vector_type(NB)));
+    sq_v4i w[NT][NB];  // Q8_0: 16 bytes of the block; Q4_0: the packed block
+    sq_v4i a[NB];
+    scales sw[NT], sa;  // the batch's f16 block scales of this lane's weight rows and activation row
 };
 
-template <int WT>
+template <int WT, int NT, int NB>
 __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const int8_t* __restrict__ aq,
                                                                const uint16_t* __restrict__ ad, int m_rows,
                                                                float* __restrict__ out, int ldo, int accumulate,
-                                                               int per) {
-    __shared__ float red[RW_NW][16][64];
+                                                               int per, int kbs, size_t split_stride) {
+    __shared__ float red[RW_NW][NT * 16][64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = w.k, KB = K >> 5;
-    const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+    const int n0 = blockIdx.x * 32 * NT, m0 = blockIdx.y * 32;
     const int fr = lane & 31, fh = lane >> 5;
-    // this wavefront's blocks [kbw, kend), per (a multiple of 2 RW_NB) per wavefront
-    const int kbw = wave * per, kend = min(KB, kbw + per);
-    const int nb = per / RW_NB;
-    const size_t wrow = (size_t)min(n0 + fr, w.rows - 1), arow = (size_t)min(m0 + fr, m_rows - 1);
-    const bool wvalid = n0 + fr < w.rows;
-
-    auto load = [&](RwBatch& B, int kb) {
-        const int kc = min(kb, KB - RW_NB);  // KB is a multiple of RW_NB
+    // the workgroup's blocks [kb_begin, kb_end) (split blockIdx.z), and this
+    // wavefront's [kbw, kend): per (a multiple of 2 NB) per wavefront
+    const int kb_begin = blockIdx.z * kbs, kb_end = min(KB, kb_begin + kbs);
+    out += blockIdx.z * split_stride;
+    const int kbw = kb_begin + wave * per, kend = min(kb_end, kbw + per);
+    const int nb = per / NB;
+    typedef RwBatch<NT, NB> Batch;
+    size_t wrow[NT];
+    bool wvalid[NT];
 #pragma unroll
-        for (int j = 0; j < RW_NB; j++) {
-            if constexpr (WT == WT_Q8_0)
-                B.w[j] = *(const sq_v4i*)((const int8_t*)w.qs + wrow * K + (kc + j) * 32 + 16 * fh);
-            else
-                B.w[j] = *(const sq_v4i*)((const uint8_t*)w.qs + wrow * (K / 2) + (kc + j) * 16);
+    for (int t = 0; t < NT; t++) {
+        wrow[t] = (size_t)min(n0 + 32 * t + fr, w.rows - 1);
+        wvalid[t] = n0 + 32 * t + fr < w.rows;
+    }
+    const size_t arow = (size_t)min(m0 + fr, m_rows - 1);
+
+    auto load = [&](Batch& B, int kb) {
+        const int kc = min(kb, KB - NB);  // KB is a multiple of NB
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                if constexpr (WT == WT_Q8_0)
+                    B.w[t][j] = *(const sq_v4i*)((const int8_t*)w.qs + wrow[t] * K + (kc + j) * 32 + 16 * fh);
+                else
+                    B.w[t][j] = *(const sq_v4i*)((const uint8_t*)w.qs + wrow[t] * (K / 2) + (kc + j) * 16);
+            }
             B.a[j] = *(const sq_v4i*)(aq + arow * K + (kc + j) * 32 + 16 * fh);
         }
-        B.sw = *(const rw_scales*)(w.scale + wrow * KB + kc);
-        B.sa = *(const rw_scales*)(ad + arow * KB + kc);
-    };
-    m8_v16f acc;
 #pragma unroll
-    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+        for (int t = 0; t < NT; t++) B.sw[t] = *(const typename Batch::scales*)(w.scale + wrow[t] * KB + kc);
+        B.sa = *(const typename Batch::scales*)(ad + arow * KB + kc);
+    };
+    m8_v16f acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
     const m8_v16i izero = {};
     const m8_v16f fzero = {};
-    auto compute = [&](const RwBatch& B, int kb) {
+    auto compute = [&](const Batch& B, int kb) {
 #pragma unroll
-        for (int j = 0; j < RW_NB; j++) {
-            sq_v4i wf = B.w[j];
-            if constexpr (WT == WT_Q4_0) {
-                // byte t holds element t (low nibble) and t + 16 (high nibble):
-                // half fh of the block is one nibble of every byte, as q - 8
-                // in a signed byte ((q | 0x80) - 8 stays within the byte, and
-                // xor 0x80 restores the sign)
-                const int sh = 4 * fh;
-                wf.x = (int)(((((unsigned)wf.x >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
-                wf.y = (int)(((((unsigned)wf.y >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
-                wf.z = (int)(((((unsigned)wf.z >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
-                wf.w = (int)(((((unsigned)wf.w >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
-            }
+        for (int j = 0; j < NB; j++) {
             // blocks past the range fold nothing: both scales zero (an
             // activation scale may be inf, and inf * 0 would not be).  Lane
             // l % 32 carries activation row l % 32 in sa and weight row
@@ -695,43 +702,60 @@ __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const 
             // (selects, not branches: a branch here lets the compiler move
             // every block's combine after all the matrix instructions)
             const bool inb = kb + j < kend && fh == 0;
-            const uint16_t sav = inb ? (uint16_t)B.sa[j] : (uint16_t)0, swv = inb && wvalid ? (uint16_t)B.sw[j] : (uint16_t)0;
             const _Float16 h0 = 0;
-            const mq_v4h sa = {__builtin_bit_cast(_Float16, sav), h0, h0, h0};
-            const mq_v4h sw = {__builtin_bit_cast(_Float16, swv), h0, h0, h0};
-            const m8_v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(B.a[j], wf, izero, 0, 0, 0);
-            const m8_v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sw, fzero, 0, 0, 0);
+            const mq_v4h sa = {__builtin_bit_cast(_Float16, inb ? (uint16_t)B.sa[j] : (uint16_t)0), h0, h0, h0};
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[r] = fmaf((float)d[r], sc[r], acc[r]);
-            // one block's products live at a time: left to itself the
-            // scheduler issues every block's matrix instructions first and
-            // spills their results
-            __builtin_amdgcn_sched_barrier(0);
+            for (int t = 0; t < NT; t++) {
+                sq_v4i wf = B.w[t][j];
+                if constexpr (WT == WT_Q4_0) {
+                    // byte i holds element i (low nibble) and i + 16 (high
+                    // nibble): half fh of the block is one nibble of every
+                    // byte, as q - 8 in a signed byte ((q | 0x80) - 8 stays
+                    // within the byte, and xor 0x80 restores the sign)
+                    const int sh = 4 * fh;
+                    wf.x = (int)(((((unsigned)wf.x >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+                    wf.y = (int)(((((unsigned)wf.y >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+                    wf.z = (int)(((((unsigned)wf.z >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+                    wf.w = (int)(((((unsigned)wf.w >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ (int)0x80808080u;
+                }
+                const uint16_t swv = inb && wvalid[t] ? (uint16_t)B.sw[t][j] : (uint16_t)0;
+                const mq_v4h sw = {__builtin_bit_cast(_Float16, swv), h0, h0, h0};
+                const m8_v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(B.a[j], wf, izero, 0, 0, 0);
+                const m8_v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sw, fzero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[t][r] = fmaf((float)d[r], sc[r], acc[t][r]);
+                // one tile's products live at a time: left to itself the
+                // scheduler issues every block's matrix instructions first and
+                // spills their results
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
-    RwBatch B0, B1;
+    Batch B0, B1;
     load(B0, kbw);
-    load(B1, kbw + RW_NB);
+    load(B1, kbw + NB);
     for (int b = 0; b + 2 < nb; b += 2) {
-        compute(B0, kbw + b * RW_NB);
-        load(B0, kbw + (b + 2) * RW_NB);
-        compute(B1, kbw + (b + 1) * RW_NB);
-        load(B1, kbw + (b + 3) * RW_NB);
+        compute(B0, kbw + b * NB);
+        load(B0, kbw + (b + 2) * NB);
+        compute(B1, kbw + (b + 1) * NB);
+        load(B1, kbw + (b + 3) * NB);
     }
-    compute(B0, kbw + (nb - 2) * RW_NB);
-    compute(B1, kbw + (nb - 1) * RW_NB);
+    compute(B0, kbw + (nb - 2) * NB);
+    compute(B1, kbw + (nb - 1) * NB);
 
-    // partial tiles summed in wavefront order; element r of lane l is row
-    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
+    // partial tiles summed in wavefront order; element r of lane l of tile t
+    // is row 8 (r / 4) + 4 (l / 32) + r % 4, column 32 t + l % 32
 #pragma unroll
-    for (int r = 0; r < 16; r++) red[wave][r][lane] = acc[r];
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) red[wave][16 * t + r][lane] = acc[t][r];
     __syncthreads();
-    for (int e = tid; e < 16 * 64; e += RW_NW * 64) {
-        const int r = e >> 6, l = e & 63;
+    for (int e = tid; e < NT * 16 * 64; e += RW_NW * 64) {
+        const int tr = e >> 6, l = e & 63, t = tr >> 4, r = tr & 15;
         float v = 0.0f;
 #pragma unroll
-        for (int q = 0; q < RW_NW; q++) v += red[q][r][l];
-        const int mm = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), nn = n0 + (l & 31);
+        for (int q = 0; q < RW_NW; q++) v += red[q][tr][l];
+        const int mm = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), nn = n0 + 32 * t + (l & 31);
         if (mm < m_rows && nn < w.rows) {
             float* o = out + (size_t)mm * ldo + nn;
             *o = accumulate ? *o + v : v;
@@ -850,19 +874,53 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
     return 0;
 }
 
-// The few-rows kernel: grid (column tiles of 32, row tiles of 32), K in
-// blocks of 32 with KB a multiple of RW_NB.
-template <int WT>
-int run_rows(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
-             bool acc) {
-    const int KB = w.k / 32;
-    const int per = ((KB + RW_NW - 1) / RW_NW + 2 * RW_NB - 1) / (2 * RW_NB) * (2 * RW_NB);
-    count_launch(1, 32);
-    hipLaunchKernelGGL(gemm_rows_kernel<WT>, dim3((w.rows + 31) / 32, (m + 31) / 32), dim3(RW_NW * 64), 0, s, w, aq,
-                       ad, m, out, ldo, acc ? 1 : 0, per);
+// The few-rows kernel: grid (column tiles of 32 NT, row tiles of 32, K
+// splits), K in blocks of 32 with KB a multiple of RW_NB.  Two column tiles
+// per workgroup where that still gives every CU a workgroup (the FFN gate/up
+// projection: twice the weights in flight per CU, one round of the grid); a
+// K split where the grid has fewer workgroups than CUs and each split keeps
+// two full batches per wavefront (the FFN down projection, K = 8192: four
+// splits).
+template <int WT, int NT>
+int launch_rows(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
+                bool acc, int gx, int gy, int splits, int kbs, float* ws) {
+    constexpr int NB = NT == 1 ? RW_NB : RW_NB / 2;
+    const int per = ((kbs + RW_NW - 1) / RW_NW + 2 * NB - 1) / (2 * NB) * (2 * NB);
+    if (splits == 1) {
+        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB>), dim3(gx, gy), dim3(RW_NW * 64), 0, s, w, aq, ad, m, out, ldo,
+                           acc ? 1 : 0, per, kbs, (size_t)0);
+    } else {
+        const size_t stride = (size_t)m * w.rows;
+        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB>), dim3(gx, gy, splits), dim3(RW_NW * 64), 0, s, w, aq, ad, m, ws,
+                           w.rows, 0, per, kbs, stride);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+        hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
+                           m, w.rows, out, ldo, acc ? 1 : 0);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
     return 0;
+}
+
+template <int WT>
+int run_rows(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
+             bool acc, float* ws, size_t ws_floats) {
+    const int KB = w.k / 32, cus = device_cus();
+    const int gy = (m + 31) / 32, tiles = (w.rows + 31) / 32;
+    const bool two = (tiles + 1) / 2 * gy >= cus;
+    const int gx = two ? (tiles + 1) / 2 : tiles;
+    int splits = 1;
+    if (ws != nullptr && gx * gy < cus) {
+        splits = min((cus + gx * gy - 1) / (gx * gy), KB / (RW_NW * 2 * RW_NB));
+        while (splits > 1 && ((size_t)splits * m * w.rows > ws_floats || KB % splits || (KB / splits) % RW_NB))
+            splits--;
+        splits = max(splits, 1);
+    }
+    const int kbs = KB / splits;
+    count_launch(splits, 32);
+    return two ? launch_rows<WT, 2>(s, w, aq, ad, m, out, ldo, acc, gx, gy, splits, kbs, ws)
+               : launch_rows<WT, 1>(s, w, aq, ad, m, out, ldo, acc, gx, gy, splits, kbs, ws);
 }
 
 // SQUIRREL_GEMM_TILE pins the prefill matmul's kernel (a test and
@@ -881,20 +939,15 @@ int gemm_tile_override() {
     return TILE_AUTO;
 }
 
-// Inputs the few-rows kernel takes unless a tiling is pinned: up to 32 rows
-// and K up to 4096.  (At K = 8192 its 32-row tiles leave the FFN down
-// projection 64 workgroups, and the 64 x 64 kernel's K split measured
-// 14.9 against 25.5 us for a 32-token prompt.)
-bool rows_kernel_fits(int m, int k) {
-    return m <= 32 && k <= 4096 && (k / 32) % RW_NB == 0 && gemm_tile_override() == TILE_AUTO;
-}
+// Inputs the few-rows kernel takes unless a tiling is pinned: up to 32 rows.
+bool rows_kernel_fits(int m, int k) { return m <= 32 && (k / 32) % RW_NB == 0 && gemm_tile_override() == TILE_AUTO; }
 
 template <int WT>
 int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
                 bool acc, float* ws, size_t ws_floats) {
     const int tile = gemm_tile_override();
     if ((tile == TILE_ROWS && (w.k / 32) % RW_NB == 0) || rows_kernel_fits(m, w.k))
-        return run_rows<WT>(s, w, aq, ad, m, out, ldo, acc);
+        return run_rows<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats);
     if (tile == TILE_128 || (tile == TILE_AUTO && m >= 128)) {
         const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128);
         if (st != 1) return st;

@@ -189,16 +189,19 @@ def test_matmul_tiles_agree(wtype, monkeypatch):
 
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
 @pytest.mark.parametrize("m,k,n,pin", [
-    (2, 2048, 2048, None), (13, 2048, 3072, None), (32, 8192, 2048, "rows"), (29, 128, 7, None),
+    (2, 2048, 2048, None), (13, 2048, 3072, None), (32, 8192, 2048, None), (29, 128, 7, None),
     (7, 512, 1000, None), (45, 2048, 512, "rows"), (200, 1024, 96, "rows"),
+    (16, 2048, 16384, None), (8, 512, 16416, None),
 ])
 def test_matmul_rows_kernel_matches_oracle(wtype, m, k, n, pin, monkeypatch):
     """The few-rows prefill matmul (inputs of at most 32 rows, or pinned with
-    SQUIRREL_GEMM_TILE=rows): 32 x 32 tiles, K split over the workgroup's
+    SQUIRREL_GEMM_TILE=rows): 32-row tiles, K split over the workgroup's
     wavefronts and summed in wavefront order.  Ragged rows and columns, K of
-    one load batch (128), and several row tiles when pinned; every output
-    within 4e-6 of its sum of |terms| of the oracle (matmul.rs:133-171), and
-    added in place with accumulate."""
+    one load batch (128), several row tiles when pinned, two column tiles per
+    workgroup on the widest matrices (16384 and 16416 rows, the latter with a
+    half-empty last pair) and a K split over workgroups at K = 8192; every
+    output within 4e-6 of its sum of |terms| of the oracle
+    (matmul.rs:133-171)."""
     if pin:
         monkeypatch.setenv("SQUIRREL_GEMM_TILE", pin)
     w, _ = quant_weights(wtype, n, k, seed=101 + m)
@@ -208,7 +211,8 @@ def test_matmul_rows_kernel_matches_oracle(wtype, m, k, n, pin, monkeypatch):
     ops.gemm_counters(reset=True)
     ops.linear(DeviceArray.from_numpy(x), W, out)
     c = ops.gemm_counters(reset=True)
-    assert c["launches"] == 1 and c["rows_launches"] == 1 and c["split_launches"] == 0, c
+    assert c["launches"] == 1 and c["rows_launches"] == 1, c
+    assert c["split_launches"] == (1 if k == 8192 else 0), c
     got = out.numpy().astype(np.float64)
     rows = np.arange(0, m, max(1, m // 9))
     want = O.linear(x[rows], wtype, w, n, O.W8A8)
