@@ -631,6 +631,12 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
 // matrix is also split over workgroups (blockIdx.z), whose partial tiles
 // split_sum_kernel adds in split order.  The per-block combine is that of
 // the other kernels: fma(f32(isum), sa * sw, acc) (dot_prod.rs:189-252).
+//
+// GU: the FFN gate/up projection with SiLU(gate) * up and its Q8_0 blocks in
+// the epilogue (two tiles: gate rows 32 j.. and the up rows ffn + 32 j..).
+// A 32-lane half of a wavefront then holds one prompt row's 32 values of
+// the FFN block j, and forms the block as silu_mul8_kernel does: the same
+// operations on the same values, so the same bits.
 constexpr int RW_NW = 8;  // wavefronts per workgroup
 constexpr int RW_NB = 4;  // blocks per load batch with one column tile (two with two)
 
@@ -642,11 +648,13 @@ struct RwBatch {
     scales sw[NT], sa;  // the batch's f16 block scales of this lane's weight rows and activation row
 };
 
-template <int WT, int NT, int NB>
+template <int WT, int NT, int NB, bool GU>
 __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const int8_t* __restrict__ aq,
                                                                const uint16_t* __restrict__ ad, int m_rows,
                                                                float* __restrict__ out, int ldo, int accumulate,
-                                                               int per, int kbs, size_t split_stride) {
+                                                               int per, int kbs, size_t split_stride,
+                                                               int8_t* __restrict__ act_q, uint16_t* __restrict__ act_d) {
+    static_assert(!GU || NT == 2, "the gate/up epilogue pairs two tiles");
     __shared__ float red[RW_NW][NT * 16][64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = w.k, KB = K >> 5;
@@ -661,10 +669,16 @@ __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const 
     typedef RwBatch<NT, NB> Batch;
     size_t wrow[NT];
     bool wvalid[NT];
+    const int ffn = w.rows / 2, j0 = blockIdx.x * 32;  // GU: the FFN block's first column
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        wrow[t] = (size_t)min(n0 + 32 * t + fr, w.rows - 1);
-        wvalid[t] = n0 + 32 * t + fr < w.rows;
+        if constexpr (GU) {
+            wvalid[t] = j0 + fr < ffn;
+            wrow[t] = (size_t)(t * ffn + min(j0 + fr, ffn - 1));
+        } else {
+            wrow[t] = (size_t)min(n0 + 32 * t + fr, w.rows - 1);
+            wvalid[t] = n0 + 32 * t + fr < w.rows;
+        }
     }
     const size_t arow = (size_t)min(m0 + fr, m_rows - 1);
 
@@ -750,6 +764,30 @@ __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const 
 #pragma unroll
         for (int r = 0; r < 16; r++) red[wave][16 * t + r][lane] = acc[t][r];
     __syncthreads();
+    if constexpr (GU) {
+        // e = 64 r + l: lanes l < 32 and l >= 32 of a wavefront are two
+        // prompt rows' FFN block j (column l % 32)
+        for (int e = tid; e < 16 * 64; e += RW_NW * 64) {
+            const int r = e >> 6, l = e & 63;
+            float g = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int q = 0; q < RW_NW; q++) {
+                g += red[q][r][l];
+                u += red[q][16 + r][l];
+            }
+            const float v = (g * sq_sigmoid(g)) * u;  // silu(gate) * up (silu_mul8_kernel)
+            float mx = fabsf(v);
+#pragma unroll
+            for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), inv = sq_q8_inv(scale);
+            const int mm = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), jj = l & 31;
+            if (mm < m_rows && j0 + jj < ffn) {
+                act_q[(size_t)mm * ffn + j0 + jj] = sq_q8_quant(v, inv);
+                if (jj == 0) act_d[(size_t)mm * (ffn / 32) + blockIdx.x] = sq_f32_to_f16(scale);
+            }
+        }
+        return;
+    }
     for (int e = tid; e < NT * 16 * 64; e += RW_NW * 64) {
         const int tr = e >> 6, l = e & 63, t = tr >> 4, r = tr & 15;
         float v = 0.0f;
@@ -881,18 +919,19 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
 // K split where the grid has fewer workgroups than CUs and each split keeps
 // two full batches per wavefront (the FFN down projection, K = 8192: four
 // splits).
-template <int WT, int NT>
+template <int WT, int NT, bool GU = false>
 int launch_rows(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
-                bool acc, int gx, int gy, int splits, int kbs, float* ws) {
+                bool acc, int gx, int gy, int splits, int kbs, float* ws, int8_t* act_q = nullptr,
+                uint16_t* act_d = nullptr) {
     constexpr int NB = NT == 1 ? RW_NB : RW_NB / 2;
     const int per = ((kbs + RW_NW - 1) / RW_NW + 2 * NB - 1) / (2 * NB) * (2 * NB);
     if (splits == 1) {
-        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB>), dim3(gx, gy), dim3(RW_NW * 64), 0, s, w, aq, ad, m, out, ldo,
-                           acc ? 1 : 0, per, kbs, (size_t)0);
+        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB, GU>), dim3(gx, gy), dim3(RW_NW * 64), 0, s, w, aq, ad, m, out,
+                           ldo, acc ? 1 : 0, per, kbs, (size_t)0, act_q, act_d);
     } else {
         const size_t stride = (size_t)m * w.rows;
-        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB>), dim3(gx, gy, splits), dim3(RW_NW * 64), 0, s, w, aq, ad, m, ws,
-                           w.rows, 0, per, kbs, stride);
+        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB, false>), dim3(gx, gy, splits), dim3(RW_NW * 64), 0, s, w, aq,
+                           ad, m, ws, w.rows, 0, per, kbs, stride, nullptr, nullptr);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
         hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
@@ -959,6 +998,19 @@ int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_
     return run_mfma<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats);
 }
 
+// The FFN gate/up projection of up to 32 prompt rows with SiLU * up and its
+// Q8_0 blocks fused (one launch instead of two); -1 when it does not apply.
+template <int WT>
+int run_gateup_silu(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, int8_t* act_q,
+                    uint16_t* act_d) {
+    const int ffn = w.rows / 2, KB = w.k / 32;
+    if (w.rows % 2 || ffn % 32 || !rows_kernel_fits(m, w.k)) return -1;
+    const int gx = ffn / 32, gy = (m + 31) / 32;
+    if (gx * gy < device_cus()) return -1;  // the split-free two-tile form only
+    count_launch(1, 32);
+    return launch_rows<WT, 2, true>(s, w, aq, ad, m, nullptr, 0, false, gx, gy, 1, KB, nullptr, act_q, act_d);
+}
+
 template <int WT, bool A8, int NBL, int MT>
 int run(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, const float* x, int m,
         float* out, int ldo, bool acc) {
@@ -1003,6 +1055,16 @@ void gemm_counters(bool reset, uint64_t* out) {
         g_tile128x64_launches = 0;
         g_rows_launches = 0;
     }
+}
+
+int launch_gateup_silu(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
+                       int8_t* act_q, uint16_t* act_d) {
+    if (w.k <= 0 || w.k % 32 != 0 || m <= 0) return -1;
+    MatView v = w;
+    v.wtype = wtype;
+    if (wtype == WT_Q8_0) return run_gateup_silu<WT_Q8_0>(s, v, aq, ad, m, act_q, act_d);
+    if (wtype == WT_Q4_0) return run_gateup_silu<WT_Q4_0>(s, v, aq, ad, m, act_q, act_d);
+    return -1;
 }
 
 int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq, const uint16_t* ad,

@@ -134,6 +134,14 @@ void gemm_counters(bool reset, uint64_t* out);
 int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_t* aq,
                 const uint16_t* ad, const float* x, int m, float* out, int ldo, bool accumulate,
                 float* ws = nullptr, size_t ws_floats = 0);
+// The FFN gate/up projection (w: [gate | up], 2 * ffn rows) of m prompt rows
+// given as Q8_0, with silu(gate) * up written as Q8_0 blocks (act_q [m][ffn],
+// act_d [m][ffn / 32]) in the same launch: what launch_gemm followed by
+// launch_silu_mul_rows writes, bit for bit.  act_q/act_d must not overlap
+// aq/ad (every workgroup reads every row).  Returns -1 (nothing launched)
+// where the fused form does not apply (more than 32 rows, small grids).
+int launch_gateup_silu(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
+                       int8_t* act_q, uint16_t* act_d);
 
 // ---- persistent decode step (k_step.hip) -----------------------------------
 struct StepLayer {

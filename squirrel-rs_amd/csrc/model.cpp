@@ -610,11 +610,11 @@ int run_prefill(sq_ctx* c, size_t n) {
         c->ptap_rows = n;
     }
     // the n rows of site j of layer l, just quantized into p_aq / p_ad
-    auto tap = [&](int l, int j, size_t k) -> int {
+    auto tap = [&](int l, int j, size_t k, const int8_t* q = nullptr, const uint16_t* d = nullptr) -> int {
         if (!taps) return 0;
         const size_t off = n * (l * TW + tap_offset(g, j));
-        SQ_HIP_CHECK(hipMemcpyAsync(c->ptap_q + off, c->p_aq, n * k, hipMemcpyDeviceToDevice, s));
-        SQ_HIP_CHECK(hipMemcpyAsync(c->ptap_d + off / 32, c->p_ad, n * k / 16, hipMemcpyDeviceToDevice, s));
+        SQ_HIP_CHECK(hipMemcpyAsync(c->ptap_q + off, q ? q : c->p_aq, n * k, hipMemcpyDeviceToDevice, s));
+        SQ_HIP_CHECK(hipMemcpyAsync(c->ptap_d + off / 32, d ? d : c->p_ad, n * k / 16, hipMemcpyDeviceToDevice, s));
         return 0;
     };
     // phase boundary for the measurement entry point (kind: 0 matmul,
@@ -664,17 +664,38 @@ int run_prefill(sq_ctx* c, size_t n) {
                                       a8 ? c->p_aq : nullptr, c->p_ad)) ||
             (st = tap(l, 2, D)))
             return st;
-        if ((st = phase(0)) ||
-            (st = launch_gemm(s, view(L.gateup), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_gu, 2 * F,
-                              false, c->p_split, kGemmSplitFloats)) ||
-            (st = phase(2)))
+        // Short prompts: gate/up, SiLU * up and its Q8_0 blocks in one launch.
+        // Every workgroup of it reads every prompt row's FFN-norm blocks in
+        // p_aq, so it writes the FFN activation's blocks apart, into p_act's
+        // bytes (unused by the integer path), and the down projection reads
+        // them there.
+        const int8_t* fq = c->p_aq;
+        const uint16_t* fd = c->p_ad;
+        int fused = -1;
+        if ((st = phase(0))) return st;
+        if (a8) {
+            int8_t* aq2 = (int8_t*)c->p_act;
+            uint16_t* ad2 = (uint16_t*)(aq2 + (size_t)N * F);
+            fused = launch_gateup_silu(s, view(L.gateup), m->wtype, c->p_aq, c->p_ad, N, aq2, ad2);
+            if (fused > 0) return fused;
+            if (fused == 0) {
+                fq = aq2;
+                fd = ad2;
+            }
+        }
+        if (fused != 0) {
+            if ((st = launch_gemm(s, view(L.gateup), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_gu, 2 * F,
+                                  false, c->p_split, kGemmSplitFloats)) ||
+                (st = phase(2)) ||
+                (st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, a8 ? nullptr : c->p_act,
+                                           a8 ? c->p_aq : nullptr, c->p_ad)))
+                return st;
+        } else if ((st = phase(2))) {
             return st;
-        if ((st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, a8 ? nullptr : c->p_act, a8 ? c->p_aq : nullptr,
-                                       c->p_ad)) ||
-            (a8 && (st = tap(l, 3, F))))
-            return st;
+        }
+        if ((a8 && (st = tap(l, 3, F, fq, fd)))) return st;
         if ((st = phase(0)) ||
-            (st = launch_gemm(s, view(L.down), m->wtype, a8, c->p_aq, c->p_ad, c->p_act, N, c->p_hidden, D, true,
+            (st = launch_gemm(s, view(L.down), m->wtype, a8, fq, fd, c->p_act, N, c->p_hidden, D, true,
                               c->p_split, kGemmSplitFloats)) ||
             (st = phase(2)))
             return st;
