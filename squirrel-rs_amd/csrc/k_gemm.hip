@@ -778,7 +778,7 @@ __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const 
             const float v = (g * sq_sigmoid(g)) * u;  // silu(gate) * up (silu_mul8_kernel)
             float mx = fabsf(v);
 #pragma unroll
-            for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
             const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), inv = sq_q8_inv(scale);
             const int mm = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), jj = l & 31;
             if (mm < m_rows && j0 + jj < ffn) {
