@@ -632,11 +632,24 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
 // split_sum_kernel adds in split order.  The per-block combine is that of
 // the other kernels: fma(f32(isum), sa * sw, acc) (dot_prod.rs:189-252).
 //
-// GU: the FFN gate/up projection with SiLU(gate) * up and its Q8_0 blocks in
-// the epilogue (two tiles: gate rows 32 j.. and the up rows ffn + 32 j..).
-// A 32-lane half of a wavefront then holds one prompt row's 32 values of
-// the FFN block j, and forms the block as silu_mul8_kernel does: the same
-// operations on the same values, so the same bits.
+// Epilogues (EPI): RW_STORE writes (or adds) the tile.  RW_GATEUP: the FFN
+// gate/up projection with SiLU(gate) * up and its Q8_0 blocks (two tiles:
+// gate rows 32 j.. and the up rows ffn + 32 j..); a 32-lane half of a
+// wavefront then holds one prompt row's 32 values of FFN block j and forms
+// the block as silu_mul8_kernel does.  RW_QKV: the stacked q|k|v projection
+// with RoPE on q and k and the KV-cache append, as rope_kv_kernel does (the
+// pair partner of column n is column n ^ 1, lane l ^ 1).  The same
+// operations on the same values, so the same bits as the separate kernels.
+enum : int { RW_STORE = 0, RW_GATEUP = 1, RW_QKV = 2 };
+struct RowsEpi {
+    int8_t* act_q;       // RW_GATEUP: FFN activation blocks [m][ffn], scales [m][ffn / 32]
+    uint16_t* act_d;
+    const float2* rope;  // RW_QKV: (cos, sin) per position and pair
+    float* q_out;        // [m][q_dim]
+    float* kcache;       // [position][kv_dim]
+    float* vcache;
+    int q_dim, kv_dim, head_dim, pos0;
+};
 constexpr int RW_NW = 8;  // wavefronts per workgroup
 constexpr int RW_NB = 4;  // blocks per load batch with one column tile (two with two)
 
@@ -648,13 +661,14 @@ struct RwBatch {
     scales sw[NT], sa;  // the batch's f16 block scales of this lane's weight rows and activation row
 };
 
-template <int WT, int NT, int NB, bool GU>
+template <int WT, int NT, int NB, int EPI>
 __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const int8_t* __restrict__ aq,
                                                                const uint16_t* __restrict__ ad, int m_rows,
                                                                float* __restrict__ out, int ldo, int accumulate,
-                                                               int per, int kbs, size_t split_stride,
-                                                               int8_t* __restrict__ act_q, uint16_t* __restrict__ act_d) {
+                                                               int per, int kbs, size_t split_stride, RowsEpi ep) {
+    constexpr bool GU = EPI == RW_GATEUP;
     static_assert(!GU || NT == 2, "the gate/up epilogue pairs two tiles");
+    static_assert(EPI != RW_QKV || NT == 1, "the q|k|v epilogue takes one tile");
     __shared__ float red[RW_NW][NT * 16][64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int K = w.k, KB = K >> 5;
@@ -782,8 +796,34 @@ __global__ __launch_bounds__(RW_NW * 64) void gemm_rows_kernel(MatView w, const 
             const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), inv = sq_q8_inv(scale);
             const int mm = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), jj = l & 31;
             if (mm < m_rows && j0 + jj < ffn) {
-                act_q[(size_t)mm * ffn + j0 + jj] = sq_q8_quant(v, inv);
-                if (jj == 0) act_d[(size_t)mm * (ffn / 32) + blockIdx.x] = sq_f32_to_f16(scale);
+                ep.act_q[(size_t)mm * ffn + j0 + jj] = sq_q8_quant(v, inv);
+                if (jj == 0) ep.act_d[(size_t)mm * (ffn / 32) + blockIdx.x] = sq_f32_to_f16(scale);
+            }
+        }
+        return;
+    }
+    if constexpr (EPI == RW_QKV) {
+        for (int e = tid; e < 16 * 64; e += RW_NW * 64) {
+            const int r = e >> 6, l = e & 63;
+            float v = 0.0f;
+#pragma unroll
+            for (int q = 0; q < RW_NW; q++) v += red[q][r][l];
+            const float pv = __shfl_xor(v, 1, 64);  // column n ^ 1 of the same prompt row
+            const int mm = m0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), n = n0 + (l & 31);
+            if (mm >= m_rows || n >= w.rows) continue;
+            const int QD = ep.q_dim, KVD = ep.kv_dim, p = ep.pos0 + mm;
+            if (n < QD + KVD) {
+                const bool is_q = n < QD;
+                const int li = is_q ? n : n - QD;
+                const float2 cs = ep.rope[(size_t)p * (ep.head_dim >> 1) + ((li % ep.head_dim) >> 1)];
+                float o0, o1;
+                if (n & 1) sq_rotate(pv, v, cs.x, cs.y, o0, o1);
+                else sq_rotate(v, pv, cs.x, cs.y, o0, o1);
+                const float o = (n & 1) ? o1 : o0;
+                if (is_q) ep.q_out[(size_t)mm * QD + li] = o;
+                else ep.kcache[(size_t)p * KVD + li] = o;
+            } else {
+                ep.vcache[(size_t)p * KVD + (n - QD - KVD)] = v;
             }
         }
         return;
@@ -919,19 +959,18 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
 // K split where the grid has fewer workgroups than CUs and each split keeps
 // two full batches per wavefront (the FFN down projection, K = 8192: four
 // splits).
-template <int WT, int NT, bool GU = false>
+template <int WT, int NT, int EPI = RW_STORE>
 int launch_rows(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
-                bool acc, int gx, int gy, int splits, int kbs, float* ws, int8_t* act_q = nullptr,
-                uint16_t* act_d = nullptr) {
+                bool acc, int gx, int gy, int splits, int kbs, float* ws, const RowsEpi& ep = RowsEpi{}) {
     constexpr int NB = NT == 1 ? RW_NB : RW_NB / 2;
     const int per = ((kbs + RW_NW - 1) / RW_NW + 2 * NB - 1) / (2 * NB) * (2 * NB);
     if (splits == 1) {
-        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB, GU>), dim3(gx, gy), dim3(RW_NW * 64), 0, s, w, aq, ad, m, out,
-                           ldo, acc ? 1 : 0, per, kbs, (size_t)0, act_q, act_d);
+        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB, EPI>), dim3(gx, gy), dim3(RW_NW * 64), 0, s, w, aq, ad, m, out,
+                           ldo, acc ? 1 : 0, per, kbs, (size_t)0, ep);
     } else {
         const size_t stride = (size_t)m * w.rows;
-        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB, false>), dim3(gx, gy, splits), dim3(RW_NW * 64), 0, s, w, aq,
-                           ad, m, ws, w.rows, 0, per, kbs, stride, nullptr, nullptr);
+        hipLaunchKernelGGL((gemm_rows_kernel<WT, NT, NB, RW_STORE>), dim3(gx, gy, splits), dim3(RW_NW * 64), 0, s, w, aq,
+                           ad, m, ws, w.rows, 0, per, kbs, stride, RowsEpi{});
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
         hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
@@ -1008,7 +1047,25 @@ int run_gateup_silu(hipStream_t s, const MatView& w, const int8_t* aq, const uin
     const int gx = ffn / 32, gy = (m + 31) / 32;
     if (gx * gy < device_cus()) return -1;  // the split-free two-tile form only
     count_launch(1, 32);
-    return launch_rows<WT, 2, true>(s, w, aq, ad, m, nullptr, 0, false, gx, gy, 1, KB, nullptr, act_q, act_d);
+    RowsEpi ep{};
+    ep.act_q = act_q;
+    ep.act_d = act_d;
+    return launch_rows<WT, 2, RW_GATEUP>(s, w, aq, ad, m, nullptr, 0, false, gx, gy, 1, KB, nullptr, ep);
+}
+
+// The stacked q|k|v projection of up to 32 prompt rows with RoPE and the
+// KV-cache append fused (one launch instead of two); -1 when it does not
+// apply.
+template <int WT>
+int run_qkv_rope(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, const RowsEpi& ep) {
+    const int KB = w.k / 32, gx = (w.rows + 31) / 32, gy = (m + 31) / 32;
+    if (!rows_kernel_fits(m, w.k) || ep.head_dim % 2 || (ep.q_dim + ep.kv_dim) % 2 ||
+        w.rows != ep.q_dim + 2 * ep.kv_dim)
+        return -1;
+    // where run_rows would pair tiles or split K (other sums than the plain path's)
+    if ((gx + 1) / 2 * gy >= device_cus() || (gx * gy < device_cus() && KB / (RW_NW * 2 * RW_NB) >= 2)) return -1;
+    count_launch(1, 32);
+    return launch_rows<WT, 1, RW_QKV>(s, w, aq, ad, m, nullptr, 0, false, gx, gy, 1, KB, nullptr, ep);
 }
 
 template <int WT, bool A8, int NBL, int MT>
@@ -1064,6 +1121,26 @@ int launch_gateup_silu(hipStream_t s, const MatView& w, int wtype, const int8_t*
     v.wtype = wtype;
     if (wtype == WT_Q8_0) return run_gateup_silu<WT_Q8_0>(s, v, aq, ad, m, act_q, act_d);
     if (wtype == WT_Q4_0) return run_gateup_silu<WT_Q4_0>(s, v, aq, ad, m, act_q, act_d);
+    return -1;
+}
+
+int launch_qkv_rope(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
+                    int q_dim, int kv_dim, int head_dim, int pos0, const float2* rope, float* q_out, float* kcache,
+                    float* vcache) {
+    if (w.k <= 0 || w.k % 32 != 0 || m <= 0) return -1;
+    MatView v = w;
+    v.wtype = wtype;
+    RowsEpi ep{};
+    ep.rope = rope;
+    ep.q_out = q_out;
+    ep.kcache = kcache;
+    ep.vcache = vcache;
+    ep.q_dim = q_dim;
+    ep.kv_dim = kv_dim;
+    ep.head_dim = head_dim;
+    ep.pos0 = pos0;
+    if (wtype == WT_Q8_0) return run_qkv_rope<WT_Q8_0>(s, v, aq, ad, m, ep);
+    if (wtype == WT_Q4_0) return run_qkv_rope<WT_Q4_0>(s, v, aq, ad, m, ep);
     return -1;
 }
 

@@ -142,6 +142,15 @@ int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_
 // where the fused form does not apply (more than 32 rows, small grids).
 int launch_gateup_silu(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
                        int8_t* act_q, uint16_t* act_d);
+// The stacked q|k|v projection (w: q_dim + 2 kv_dim rows) of m prompt rows
+// at positions pos0.. given as Q8_0, with RoPE on q and k and the KV-cache
+// append in the same launch: what launch_gemm followed by
+// launch_rope_kv_rows writes, bit for bit (q_out [m][q_dim], the caches
+// [position][kv_dim]).  Returns -1 (nothing launched) where the fused form
+// does not apply (more than 32 rows).
+int launch_qkv_rope(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
+                    int q_dim, int kv_dim, int head_dim, int pos0, const float2* rope, float* q_out, float* kcache,
+                    float* vcache);
 
 // ---- persistent decode step (k_step.hip) -----------------------------------
 struct StepLayer {

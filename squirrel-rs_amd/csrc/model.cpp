@@ -642,13 +642,21 @@ int run_prefill(sq_ctx* c, size_t n) {
                                       a8 ? c->p_aq : nullptr, c->p_ad)) ||
             (st = tap(l, 0, D)))
             return st;
-        if ((st = phase(0)) ||
-            (st = launch_gemm(s, view(L.qkv), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_qkv,
-                              QD + 2 * KVD, false, c->p_split, kGemmSplitFloats)) ||
-            (st = phase(2)))
+        // short prompts: the q|k|v projection, RoPE and the KV append in one launch
+        if ((st = phase(0))) return st;
+        const int fused_qkv = a8 ? launch_qkv_rope(s, view(L.qkv), m->wtype, c->p_aq, c->p_ad, N, QD, KVD, hd, pos0,
+                                                   c->rope, c->p_q, kc, vc)
+                                 : -1;
+        if (fused_qkv > 0) return fused_qkv;
+        if (fused_qkv != 0) {
+            if ((st = launch_gemm(s, view(L.qkv), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_qkv,
+                                  QD + 2 * KVD, false, c->p_split, kGemmSplitFloats)) ||
+                (st = phase(2)) ||
+                (st = launch_rope_kv_rows(s, c->p_qkv, QD + 2 * KVD, N, QD, KVD, hd, pos0, c->rope, c->p_q, kc, vc)))
+                return st;
+        } else if ((st = phase(2))) {
             return st;
-        if ((st = launch_rope_kv_rows(s, c->p_qkv, QD + 2 * KVD, N, QD, KVD, hd, pos0, c->rope, c->p_q, kc, vc)))
-            return st;
+        }
         if ((st = phase(1)) ||
             (st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd, c->p_attn)) ||
             (st = phase(2)))

@@ -651,24 +651,25 @@ def test_full_size_q4_0_prompt_128_decode_255(model_dir):
 
 @FULL
 @pytest.mark.parametrize("wtype", ["Q8_0", "Q4_0"])
-def test_short_prompt_fused_gateup_silu_bit_exact(model_dir, wtype, monkeypatch):
-    """1B widths (2 layers), a 32-token prompt: the FFN gate/up projection
-    runs with SiLU * up and its Q8_0 blocks fused into the matmul (256
-    workgroups of two 32-row tiles).  Pinned to the same few-rows matmul
-    kernels (SQUIRREL_GEMM_TILE=rows), which turns the fusion off, the prefill
-    and the decode steps after it give the same logits bit for bit."""
+def test_short_prompt_fused_epilogues_bit_exact(model_dir, wtype, monkeypatch):
+    """1B widths (2 layers), a 32-token prompt: the q|k|v projection runs
+    with RoPE and the KV-cache append in its epilogue, and the FFN gate/up
+    projection with SiLU * up and its Q8_0 blocks (256 workgroups of two
+    32-row tiles).  Pinned to the same few-rows matmul kernels
+    (SQUIRREL_GEMM_TILE=rows), which turns both fusions off, the prefill and
+    the decode steps after it give the same logits bit for bit."""
     from sqhip import ops
     path = full_model(model_dir, wtype, n_layers=2)
     seq = full_seq(32, 3, 5)
     ops.gemm_counters(reset=True)
     fused, toks_f, _ = run_gpu(path, seq, max_pos=64, taps=False)
     n = ops.gemm_counters(reset=True)
-    assert n["rows_launches"] == 2 * 4 and n["launches"] == 2 * 4, n   # gate/up fused: one launch, not two
+    assert n["rows_launches"] == 2 * 4 and n["launches"] == 2 * 4, n   # q|k|v, o, gate/up, down
     monkeypatch.setenv("SQUIRREL_GEMM_TILE", "rows")
     plain, toks_p, _ = run_gpu(path, seq, max_pos=64, taps=False)
     assert toks_f == toks_p
     for step, (a, b) in enumerate(zip(fused, plain)):
-        assert np.array_equal(a, b), f"step {step}: the fused and the two-launch forms differ"
+        assert np.array_equal(a, b), f"step {step}: the fused and the separate forms differ"
 
 
 @FULL
