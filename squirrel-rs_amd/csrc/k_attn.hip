@@ -165,7 +165,8 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
                                                             const float* __restrict__ kc,
                                                             const float* __restrict__ vc, int pos0,
                                                             int m_rows, int n_heads, int n_kv_heads,
-                                                            float* __restrict__ out) {
+                                                            float* __restrict__ out, int8_t* __restrict__ act_q,
+                                                            uint16_t* __restrict__ act_d) {
     __shared__ __attribute__((aligned(16))) float s_k[PT][ALD];   // [key][dim]
     __shared__ __attribute__((aligned(16))) float s_vt[HD][ALD];  // [dim][key]
 
@@ -347,12 +348,44 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
     }
     float lrow = lpart + __shfl_xor(lpart, 16, 64);
     lrow += __shfl_xor(lrow, 32, 64);
-    if (tq < m_rows) {
-        const float inv = 1.0f / lrow;
+    const float inv = 1.0f / lrow;
+    float y[4][4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) y[dt][c] = o[dt][c] * inv;
+    if (out != nullptr && tq < m_rows) {
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
             float* dst = out + (size_t)tq * q_dim + h * HD + 16 * dt + 4 * lk;
-            *(float4*)dst = make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+            *(float4*)dst = make_float4(y[dt][0], y[dt][1], y[dt][2], y[dt][3]);
+        }
+    }
+    if (act_q != nullptr) {
+        // The row's Q8_0 blocks (the o projection's input), as quantize8_kernel
+        // forms them from the stored row: block b of this head is dims
+        // 32 b .. 32 b + 31, eight on each of the lanes li + 16 lk (dt = 2 b,
+        // 2 b + 1); their maximum over those four lanes.
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int dt = 2 * b; dt < 2 * b + 2; dt++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) mx = fmaxf(mx, fabsf(y[dt][c]));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), qinv = sq_q8_inv(scale);
+            if (tq < m_rows) {
+#pragma unroll
+                for (int dt = 2 * b; dt < 2 * b + 2; dt++) {
+                    unsigned wq = 0;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) wq |= (unsigned)(uint8_t)sq_q8_quant(y[dt][c], qinv) << (8 * c);
+                    *(unsigned*)(act_q + (size_t)tq * q_dim + h * HD + 16 * dt + 4 * lk) = wq;
+                }
+                if (lk == 0) act_d[(size_t)tq * (q_dim / 32) + h * (HD / 32) + b] = sq_f32_to_f16(scale);
+            }
         }
     }
 }
@@ -421,11 +454,12 @@ int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const
 }
 
 int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, const float* vcache, int pos0,
-                        int m, int n_heads, int n_kv_heads, int head_dim, float* out) {
+                        int m, int n_heads, int n_kv_heads, int head_dim, float* out, int8_t* act_q,
+                        uint16_t* act_d) {
     if (head_dim != HD) return set_error(SQ_ERR_UNSUPPORTED, "attention kernels are built for head_dim 64");
     dim3 grid(n_heads, (m + PT - 1) / PT);
     hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos0, m, n_heads,
-                       n_kv_heads, out);
+                       n_kv_heads, out, act_q, act_d);
     return check_launch("attn_prefill");
 }
 

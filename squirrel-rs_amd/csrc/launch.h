@@ -74,9 +74,12 @@ int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const
                        float* part_m, float* part_l, float* part_o, unsigned* counters, float* attn,
                        int8_t* act_q, uint16_t* act_d);
 // Prefill: m query rows at positions pos0 .. pos0+m-1 against keys 0..pos0+m-1.
+// Writes the rows to out and/or, when act_q is non-null, their Q8_0 blocks
+// ([m][n_heads*64] and [m][n_heads*2]: what launch_quantize_rows makes of
+// out, bit for bit); either may be null.
 int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, const float* vcache,
                         int pos0, int m, int n_heads, int n_kv_heads, int head_dim,
-                        float* out);
+                        float* out, int8_t* act_q = nullptr, uint16_t* act_d = nullptr);
 // Any head_dim: one wavefront per (query, head) row; op-level entry point.
 int launch_sdpa_generic(hipStream_t s, const float* q, const float* k, const float* v, float* out,
                         int seq_q, int seq_k, int n_heads, int n_kv_heads, int head_dim);

@@ -657,12 +657,14 @@ int run_prefill(sq_ctx* c, size_t n) {
         } else if ((st = phase(2))) {
             return st;
         }
+        // the integer path takes the attention rows as Q8_0 blocks, formed by
+        // the attention kernel itself (the f32 rows are not stored)
         if ((st = phase(1)) ||
-            (st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd, c->p_attn)) ||
+            (st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd,
+                                      a8 ? nullptr : c->p_attn, a8 ? c->p_aq : nullptr, a8 ? c->p_ad : nullptr)) ||
             (st = phase(2)))
             return st;
-        if (a8 && ((st = launch_quantize_rows(s, c->p_attn, (size_t)N * QD, c->p_aq, c->p_ad)) || (st = tap(l, 1, QD))))
-            return st;
+        if (a8 && (st = tap(l, 1, QD))) return st;
         if ((st = phase(0)) ||
             (st = launch_gemm(s, view(L.o), m->wtype, a8, c->p_aq, c->p_ad, c->p_attn, N, c->p_hidden, D, true,
                               c->p_split, kGemmSplitFloats)) ||
