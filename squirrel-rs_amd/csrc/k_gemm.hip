@@ -602,6 +602,330 @@ __global__ __launch_bounds__(256, (m8_occupancy<BM, BN>())) void gemm_mfma32_ker
         }
 }
 
+// Matmul epilogues: RW_STORE writes (or adds) the tile; RW_GATEUP and RW_QKV
+// are described with the kernels that take them.
+enum : int { RW_STORE = 0, RW_GATEUP = 1, RW_QKV = 2 };
+struct RowsEpi {
+    int8_t* act_q;       // RW_GATEUP: FFN activation blocks [m][ffn], scales [m][ffn / 32]
+    uint16_t* act_d;
+    const float2* rope;  // RW_QKV: (cos, sin) per position and pair
+    float* q_out;        // [m][q_dim]
+    float* kcache;       // [position][kv_dim]
+    float* vcache;
+    int q_dim, kv_dim, head_dim, pos0;
+};
+// ---- the same contraction with direct global -> LDS loads ---------------------
+// gemm_dma_kernel computes what gemm_mfma32_kernel computes, with the same
+// matrix instructions folding the same per-block terms in the same order
+// (so both give the same bits), but its tiles never pass through registers:
+// global_load_lds_dwordx4 writes each 64-lane load (1 KB) straight into one
+// of ST LDS stages, and the loads run ST - 1 chunks ahead of the chunk being
+// multiplied.  Without staging registers the kernel fits three workgroups per
+// CU.  A stage holds, for one chunk of two blocks (64 bytes of K per row), the
+// BM activation rows and BN weight rows (Q8_0 payload) and one 32-bit word of
+// the two blocks' fp16 scales per row.  Row r's four 16-byte units are stored
+// with unit u at position u ^ ((r >> 1) & 3): the 16-byte operand reads of
+// eight consecutive rows at one unit then fall in distinct banks.  Each stage
+// is its own LDS object, so the compiler's wait before reading one stage
+// does not wait for the loads still in flight into the others; a bare
+// s_barrier (no fence, which would wait for every load in flight) follows
+// each wavefront's own wait for the stage's loads.  Needs an even block
+// count per K range (K a multiple of 64).
+//
+// Epilogues: RW_GATEUP (128 x 128 tiles) takes the stacked [gate; up]
+// matrix with column tile x holding gate rows 64 x + 32 h .. + 31 and the
+// same up rows in its tiles 2 h and 2 h + 1 (h the wavefront's column half),
+// so every output element of a wavefront's gate tile has its up value at the
+// same register of the next tile; the 32 lanes of a half-wavefront then hold
+// one prompt row's FFN block, and SiLU(gate) * up and its Q8_0 block are
+// formed as silu_mul8_kernel forms them.  RW_QKV (128 x 64 tiles) applies
+// RoPE to the q and k columns (the pair partner of column n is column n ^ 1,
+// lane l ^ 1) and appends the K and V rows to the cache, as rope_kv_kernel
+// does.  The same operations on the same values as the separate kernels, so
+// the same bits.
+template <int BM, int BN>
+struct DmaStage {
+    int8_t a[BM * M8_KC];
+    int8_t w[BN * M8_KC];
+    uint32_t sa[BM];  // sa_b0 | sa_b1 << 16
+    uint32_t sw[BN];
+};
+
+__device__ __forceinline__ int dma_swz(int r) { return (r >> 1) & 3; }
+
+// A direct global -> LDS load (global_load_lds_dwordx4 for 16 bytes per lane,
+// global_load_lds_dword for 4): lane l's bytes land at lds + SIZE * l (lds is
+// the same on every lane: it goes to M0).  Issued from inline assembly, so
+// the compiler's wait-count pass does not see it: that pass cannot tell
+// which stage such a load writes once a loop merges its state, and would
+// make every read of any stage wait for every load in flight.  The caller
+// waits for the loads itself (s_waitcnt vmcnt) before a barrier.
+template <int SIZE>
+__device__ __forceinline__ void dma_to_lds(const void* src, const void* lds) {
+    static_assert(SIZE == 4 || SIZE == 16, "dword or dwordx4");
+    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) const void*)lds);
+    if constexpr (SIZE == 16)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+}
+
+// s_waitcnt immediate: at most n vector-memory operations outstanding (the
+// LDS and export counters not waited on).
+constexpr int dma_vmcnt(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// SQUIRREL_GEMM_DMA=0 keeps the full-rate tilings on the register-staged
+// kernel (a test and measurement aid: both give the same bits).
+bool gemm_dma_enabled() {
+    const char* e = getenv("SQUIRREL_GEMM_DMA");
+    return !(e && !strcmp(e, "0"));
+}
+
+template <int BM, int BN, int ST>
+constexpr int dma_occupancy() { return BN == 128 ? 2 : 3; }
+constexpr int DMA_STAGES = 3;
+
+template <int BM, int BN, int ST, int EPI>
+__global__ __launch_bounds__(256, (dma_occupancy<BM, BN, ST>())) void gemm_dma_kernel(
+    MatView w, const int8_t* __restrict__ aq, const uint16_t* __restrict__ ad, int m_rows,
+    float* __restrict__ out, int ldo, int accumulate, int kbs, size_t split_stride, RowsEpi ep) {
+    static_assert(BM == 128 && (BN == 64 || BN == 128), "tiles of 128 x 128 or 128 x 64");
+    static_assert(EPI != RW_GATEUP || BN == 128, "the gate/up epilogue takes 128 x 128 tiles");
+    static_assert(EPI != RW_QKV || BN == 64, "the q|k|v epilogue takes 128 x 64 tiles");
+    static_assert(ST >= 2 && ST <= 4, "two to four stages");
+    constexpr int SM = BM / 64, SN = BN / 64;
+    constexpr int NT = SM * SN;
+    constexpr int LA = BM / 64, LW = BN / 64;  // 1 KB payload loads per wavefront and stage
+    constexpr int LPW = LA + LW + 1;           // loads per wavefront and stage (one scale load)
+    __shared__ __attribute__((aligned(16))) DmaStage<BM, BN> st0, st1, st2, st3;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int K = w.k, KB = K >> 5;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb_begin = blockIdx.z * kbs, kb_end = min(KB, kb_begin + kbs);
+    out += blockIdx.z * split_stride;
+    const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+    const int fr = lane & 31, fh = lane >> 5;
+
+    // Per-lane source offsets of this wavefront's loads, at block 0.  Load q
+    // of a stage's payload covers rows 16 q .. 16 q + 15; lane j writes unit
+    // j % 4 of row 16 q + j / 4, which holds logical unit (j % 4) ^ swz(row).
+    size_t offa[LA], offw[LW];
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+        const int q = wave + 4 * i, r = 16 * q + (lane >> 2), u = (lane & 3) ^ dma_swz(r);
+        offa[i] = (size_t)min(m0 + r, m_rows - 1) * K + 16 * u;
+    }
+    const int ffn = w.rows / 2;  // RW_GATEUP: FFN width
+#pragma unroll
+    for (int i = 0; i < LW; i++) {
+        const int q = wave + 4 * i, r = 16 * q + (lane >> 2), u = (lane & 3) ^ dma_swz(r);
+        int row = min(n0 + r, w.rows - 1);
+        if constexpr (EPI == RW_GATEUP)
+            row = ((r >> 5) & 1) * ffn + min(64 * (int)blockIdx.x + 32 * (r >> 6) + (r & 31), ffn - 1);
+        offw[i] = (size_t)row * K + 16 * u;
+    }
+    // The scale words: waves 0 and 1 take the activation rows 64 v .. 64 v +
+    // 63; waves 2 and 3 the weight rows (with 64 columns, 32 rows each, on
+    // lanes 0-31).
+    const bool sc_act = wave < 2;
+    const int sc_row = sc_act ? 64 * wave + lane : (BN == 128 ? 64 * (wave - 2) + lane : 32 * (wave - 2) + lane);
+    const bool sc_on = sc_act || BN == 128 || lane < 32;
+    int sc_wrow = min(n0 + sc_row, w.rows - 1);
+    if constexpr (EPI == RW_GATEUP)
+        sc_wrow = ((sc_row >> 5) & 1) * ffn + min(64 * (int)blockIdx.x + 32 * (sc_row >> 6) + (sc_row & 31), ffn - 1);
+    const size_t offs = sc_act ? (size_t)min(m0 + sc_row, m_rows - 1) * KB : (size_t)sc_wrow * KB;
+    const uint16_t* sc_src = sc_act ? ad : w.scale;
+    const int sc_dst = sc_act ? 64 * wave : (BN == 128 ? 64 * (wave - 2) : 32 * (wave - 2));
+
+    auto issue = [&](DmaStage<BM, BN>& S, int kb0) {
+#pragma unroll
+        for (int i = 0; i < LA; i++) dma_to_lds<16>(aq + offa[i] + (size_t)kb0 * 32, S.a + 1024 * (wave + 4 * i));
+#pragma unroll
+        for (int i = 0; i < LW; i++)
+            dma_to_lds<16>((const int8_t*)w.qs + offw[i] + (size_t)kb0 * 32, S.w + 1024 * (wave + 4 * i));
+        if (sc_on) dma_to_lds<4>(sc_src + offs + kb0, (sc_act ? S.sa : S.sw) + sc_dst);
+    };
+
+    m8_v16f acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+
+    // Operand addresses within a stage (bytes), for block 0 and row tile i /
+    // column tile j; block 1 is unit 2 + fh, which XORs the same way.
+    int ra[SM], rw[SN];
+#pragma unroll
+    for (int i = 0; i < SM; i++) {
+        const int r = wm + 32 * i + fr;
+        ra[i] = r * M8_KC;
+    }
+#pragma unroll
+    for (int j = 0; j < SN; j++) {
+        const int r = wn + 32 * j + fr;
+        rw[j] = r * M8_KC;
+    }
+    const int ua0 = 16 * (fh ^ dma_swz(fr)), ua1 = 16 * ((2 + fh) ^ dma_swz(fr));
+    const uint32_t lo_mask = fh ? 0u : 0xFFFFFFFFu;  // k-slots 4-7 (lanes 32-63) are zero
+    // (wm, wn and 32 i, 32 j are multiples of 8, so swz depends on fr alone)
+
+    auto compute = [&](const DmaStage<BM, BN>& S) {
+        // scale operands: lanes 0-31 hold k-slots 0-3 of row (column) fr, the
+        // others slots 4-7 (zero).  Block 0 pairs (sa_b0, 0) with (sw_b0,
+        // sw_b1); block 1 pairs (0, sa_b1) with the same.
+        uint32_t sar[SM], swr[SN];
+#pragma unroll
+        for (int i = 0; i < SM; i++) sar[i] = S.sa[wm + 32 * i + fr] & lo_mask;
+#pragma unroll
+        for (int j = 0; j < SN; j++) swr[j] = S.sw[wn + 32 * j + fr] & lo_mask;
+        sq_v4i af[SM], bf[SN];
+        auto operands = [&](int b) {
+            const int ua = b ? ua1 : ua0;
+#pragma unroll
+            for (int i = 0; i < SM; i++) af[i] = *(const sq_v4i*)(S.a + ra[i] + ua);
+#pragma unroll
+            for (int j = 0; j < SN; j++) bf[j] = *(const sq_v4i*)(S.w + rw[j] + ua);
+        };
+        auto sa_op = [&](int b, int i) {
+            const uint32_t v = b ? (sar[i] & 0xFFFF0000u) : (sar[i] & 0xFFFFu);
+            return __builtin_bit_cast(mq_v4h, make_uint2(v, 0u));
+        };
+        auto sw_op = [&](int j) { return __builtin_bit_cast(mq_v4h, make_uint2(swr[j], 0u)); };
+        const m8_v16i izero = {};
+        const m8_v16f fzero = {};
+        m8_v16i d[2];
+        m8_v16f sc[2];
+        operands(0);
+        d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0], bf[0], izero, 0, 0, 0);
+        sc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa_op(0, 0), sw_op(0), fzero, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < NT * M8_KB; k++) {
+            if (k + 1 < NT * M8_KB) {
+                const int t1 = (k + 1) % NT, i = t1 / SN, j = t1 % SN, b1 = (k + 1) / NT;
+                if (t1 == 0) operands(b1);
+                d[(k + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], izero, 0, 0, 0);
+                sc[(k + 1) & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa_op(b1, i), sw_op(j), fzero, 0, 0, 0);
+            }
+            if constexpr (BN == 128) __builtin_amdgcn_sched_barrier(0);
+            const int t = k % NT;
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][r] = fmaf((float)d[k & 1][r], sc[k & 1][r], acc[t][r]);
+            if constexpr (BN == 128) __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Wait until this wavefront's loads of the chunk about to be multiplied
+    // have landed: `ahead` later chunks' loads may stay in flight.
+    auto wait_stage = [&](int ahead) {
+        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(dma_vmcnt(2 * LPW));
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(dma_vmcnt(LPW));
+        else __builtin_amdgcn_s_waitcnt(dma_vmcnt(0));
+    };
+    // (every LDS read of a stage is consumed by a matrix instruction before
+    // the wavefront reaches the next barrier, so no read is still in flight
+    // when another wavefront's loads overwrite the stage)
+    auto barrier = [] {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    // One chunk: wait for its stage, then refill the stage the previous chunk
+    // used and multiply this one.  Each call site names its LDS objects
+    // directly, so the compiler's wait before the stage's reads covers only
+    // that stage's loads.
+    const int n = (kb_end - kb_begin) / M8_KB;
+    auto chunk = [&](int cc, DmaStage<BM, BN>& cur, DmaStage<BM, BN>& refill) {
+        if (cc < n) {
+            wait_stage(min(ST - 2, n - 1 - cc));
+            barrier();
+            if (cc + ST - 1 < n) issue(refill, kb_begin + M8_KB * (cc + ST - 1));
+            compute(cur);
+        }
+    };
+    // the first ST - 1 chunks' loads
+    if (0 < n) issue(st0, kb_begin);
+    if constexpr (ST >= 3)
+        if (1 < n) issue(st1, kb_begin + M8_KB);
+    if constexpr (ST >= 4)
+        if (2 < n) issue(st2, kb_begin + 2 * M8_KB);
+    for (int c = 0; c < n; c += ST) {
+        if constexpr (ST == 2) {
+            chunk(c, st0, st1);
+            chunk(c + 1, st1, st0);
+        } else if constexpr (ST == 3) {
+            chunk(c, st0, st2);
+            chunk(c + 1, st1, st0);
+            chunk(c + 2, st2, st1);
+        } else {
+            chunk(c, st0, st3);
+            chunk(c + 1, st1, st0);
+            chunk(c + 2, st2, st1);
+            chunk(c + 3, st3, st2);
+        }
+    }
+    // element r of tile t is row 8 (r / 4) + 4 fh + r % 4 of row tile t / SN,
+    // column fr of column tile t % SN
+    if constexpr (EPI == RW_GATEUP) {
+        const int f = 64 * blockIdx.x + 32 * (wave & 1) + fr;  // FFN column
+#pragma unroll
+        for (int i = 0; i < SM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float g = acc[SN * i][r], u = acc[SN * i + 1][r];
+                const float v = (g * sq_sigmoid(g)) * u;  // silu(gate) * up (silu_mul8_kernel)
+                float mx = fabsf(v);
+#pragma unroll
+                for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+                const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), inv = sq_q8_inv(scale);
+                const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
+                if (m < m_rows && f < ffn) {
+                    ep.act_q[(size_t)m * ffn + f] = sq_q8_quant(v, inv);
+                    if (fr == 0) ep.act_d[(size_t)m * (ffn / 32) + f / 32] = sq_f32_to_f16(scale);
+                }
+            }
+        return;
+    }
+    if constexpr (EPI == RW_QKV) {
+        const int QD = ep.q_dim, KVD = ep.kv_dim, n = n0 + wn + fr;
+#pragma unroll
+        for (int i = 0; i < SM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float v = acc[i][r];
+                const float pv = __shfl_xor(v, 1, 64);  // column n ^ 1 of the same prompt row
+                const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
+                if (m >= m_rows || n >= w.rows) continue;
+                const int p = ep.pos0 + m;
+                if (n < QD + KVD) {
+                    const bool is_q = n < QD;
+                    const int li = is_q ? n : n - QD;
+                    const float2 cs = ep.rope[(size_t)p * (ep.head_dim >> 1) + ((li % ep.head_dim) >> 1)];
+                    float o0, o1;
+                    if (n & 1) sq_rotate(pv, v, cs.x, cs.y, o0, o1);
+                    else sq_rotate(v, pv, cs.x, cs.y, o0, o1);
+                    const float o = (n & 1) ? o1 : o0;
+                    if (is_q) ep.q_out[(size_t)m * QD + li] = o;
+                    else ep.kcache[(size_t)p * KVD + li] = o;
+                } else {
+                    ep.vcache[(size_t)p * KVD + (n - QD - KVD)] = v;
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = m0 + wm + 32 * (t / SN) + 8 * (r >> 2) + 4 * fh + (r & 3);
+            const int n2 = n0 + wn + 32 * (t % SN) + fr;
+            if (m < m_rows && n2 < w.rows) {
+                float* o = out + (size_t)m * ldo + n2;
+                *o = accumulate ? *o + acc[t][r] : acc[t][r];
+            }
+        }
+}
+
 // out[r, c] (+)= the sum of the K-split partial tiles, in split order.
 __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ ws, int splits, size_t stride,
                                                         int m, int n, float* __restrict__ out, int ldo,
@@ -640,16 +964,6 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
 // with RoPE on q and k and the KV-cache append, as rope_kv_kernel does (the
 // pair partner of column n is column n ^ 1, lane l ^ 1).  The same
 // operations on the same values, so the same bits as the separate kernels.
-enum : int { RW_STORE = 0, RW_GATEUP = 1, RW_QKV = 2 };
-struct RowsEpi {
-    int8_t* act_q;       // RW_GATEUP: FFN activation blocks [m][ffn], scales [m][ffn / 32]
-    uint16_t* act_d;
-    const float2* rope;  // RW_QKV: (cos, sin) per position and pair
-    float* q_out;        // [m][q_dim]
-    float* kcache;       // [position][kv_dim]
-    float* vcache;
-    int q_dim, kv_dim, head_dim, pos0;
-};
 constexpr int RW_NW = 8;  // wavefronts per workgroup
 constexpr int RW_NB = 4;  // blocks per load batch with one column tile (two with two)
 
@@ -934,14 +1248,26 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
     const int kbs = ((chunks + splits - 1) / splits) * M8_KB;
     splits = (KB + kbs - 1) / kbs;
     count_launch(splits, BN);
+    // Q8_0 weights with an even block count take the direct-to-LDS kernel
+    // (the same results); Q4_0 nibbles are expanded while staging.
+    const bool dma = WT == WT_Q8_0 && KB % 2 == 0 && gemm_dma_enabled();
+    constexpr int ST = DMA_STAGES;
     hipError_t e;
     if (splits == 1) {
-        hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo,
-                           acc ? 1 : 0, KB, (size_t)0);
+        if (dma)
+            hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, ST, RW_STORE>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m,
+                               out, ldo, acc ? 1 : 0, KB, (size_t)0, RowsEpi{});
+        else
+            hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo,
+                               acc ? 1 : 0, KB, (size_t)0);
     } else {
         const size_t stride = (size_t)m * w.rows;
-        hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy, splits), dim3(256), 0, s, w, aq, ad, m, ws,
-                           w.rows, 0, kbs, stride);
+        if (dma)
+            hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, ST, RW_STORE>), dim3(gx, gy, splits), dim3(256), 0, s, w, aq,
+                               ad, m, ws, w.rows, 0, kbs, stride, RowsEpi{});
+        else
+            hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy, splits), dim3(256), 0, s, w, aq, ad, m,
+                               ws, w.rows, 0, kbs, stride);
         e = hipGetLastError();
         if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
         hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
@@ -1037,13 +1363,50 @@ int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_
     return run_mfma<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats);
 }
 
-// The FFN gate/up projection of up to 32 prompt rows with SiLU * up and its
-// Q8_0 blocks fused (one launch instead of two); -1 when it does not apply.
+// SQUIRREL_PREFILL_UNFUSED=1 turns the fused gate/up and q|k|v epilogues
+// off (a test aid: the separate kernels give the same bits).
+bool prefill_fusion_enabled() {
+    const char* e = getenv("SQUIRREL_PREFILL_UNFUSED");
+    return !(e && !strcmp(e, "1"));
+}
+
+// The direct-to-LDS kernel with a fused epilogue, where the unfused path
+// would run that kernel on the same tiles with no K split (Q8_0, an even
+// block count, a grid of at least two workgroups per CU and no pinned
+// tiling); -1 when it does not apply.
+template <int BN, int EPI>
+int run_dma_fused(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, int gx,
+                  const RowsEpi& ep) {
+    const int KB = w.k / 32, gy = (m + 127) / 128;
+    if (w.wtype != WT_Q8_0 || KB % 2 || !gemm_dma_enabled() || gemm_tile_override() != TILE_AUTO) return -1;
+    if (gx * gy < 2 * device_cus()) return -1;
+    // the unfused path's choice for this grid: 128 x 128 tiles where those
+    // fill the device, else 128 x 64
+    const int g128 = (w.rows + 127) / 128 * gy;
+    if ((BN == 128) != (g128 >= 2 * device_cus())) return -1;
+    count_launch(1, BN);
+    hipLaunchKernelGGL((gemm_dma_kernel<128, BN, DMA_STAGES, EPI>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m,
+                       nullptr, 0, 0, KB, (size_t)0, ep);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+    return 0;
+}
+
+// The FFN gate/up projection with SiLU * up and its Q8_0 blocks fused (one
+// launch instead of two): up to 32 prompt rows on the few-rows kernel, long
+// prompts on the direct-to-LDS kernel; -1 when it does not apply.
 template <int WT>
 int run_gateup_silu(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, int8_t* act_q,
                     uint16_t* act_d) {
     const int ffn = w.rows / 2, KB = w.k / 32;
-    if (w.rows % 2 || ffn % 32 || !rows_kernel_fits(m, w.k)) return -1;
+    if (w.rows % 2 || ffn % 32 || !prefill_fusion_enabled()) return -1;
+    if (!rows_kernel_fits(m, w.k)) {
+        if (ffn % 64) return -1;
+        RowsEpi ep{};
+        ep.act_q = act_q;
+        ep.act_d = act_d;
+        return run_dma_fused<128, RW_GATEUP>(s, w, aq, ad, m, ffn / 64, ep);
+    }
     const int gx = ffn / 32, gy = (m + 31) / 32;
     if (gx * gy < device_cus()) return -1;  // the split-free two-tile form only
     count_launch(1, 32);
@@ -1059,9 +1422,10 @@ int run_gateup_silu(hipStream_t s, const MatView& w, const int8_t* aq, const uin
 template <int WT>
 int run_qkv_rope(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, const RowsEpi& ep) {
     const int KB = w.k / 32, gx = (w.rows + 31) / 32, gy = (m + 31) / 32;
-    if (!rows_kernel_fits(m, w.k) || ep.head_dim % 2 || (ep.q_dim + ep.kv_dim) % 2 ||
-        w.rows != ep.q_dim + 2 * ep.kv_dim)
+    if (ep.head_dim % 2 || (ep.q_dim + ep.kv_dim) % 2 || w.rows != ep.q_dim + 2 * ep.kv_dim ||
+        !prefill_fusion_enabled())
         return -1;
+    if (!rows_kernel_fits(m, w.k)) return run_dma_fused<64, RW_QKV>(s, w, aq, ad, m, (w.rows + 63) / 64, ep);
     // where run_rows would pair tiles or split K (other sums than the plain path's)
     if ((gx + 1) / 2 * gy >= device_cus() || (gx * gy < device_cus() && KB / (RW_NW * 2 * RW_NB) >= 2)) return -1;
     count_launch(1, 32);

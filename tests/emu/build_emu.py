@@ -11,7 +11,8 @@ launcher then stops the run with a sanitizer report naming the access.
 Source rewrites, applied to copies under _build/src: dynamic
 `extern __shared__` arrays become pointers to the launch's dynamic LDS,
 `asm volatile` wait-count statements (no effect on the emulated memory
-model) are dropped, and the library's refusals of the f32-activation
+model) are dropped (the direct-to-LDS load helper's assembly becomes the
+emulated load), and the library's refusals of the f32-activation
 kernels (switched off on the device; see kA32Disabled) are removed so that
 those kernels can be checked here.
 
@@ -41,6 +42,10 @@ SKIP = {"k_step.hip"}
 def rewrite(text: str) -> str:
     text = re.sub(r"extern\s+__shared__\s+(\w+)\s+(\w+)\s*\[\s*\]\s*;",
                   r"\1* \2 = (\1*)::sqemu::dyn_lds();", text)
+    # the direct-to-LDS load helper issues its load from inline assembly:
+    # here the emulated load does the copy
+    text = re.sub(r"(void dma_to_lds\(const void\* src, const void\* lds\) \{)",
+                  r"\1\n    ::sqemu::global_load_lds(src, (void*)lds, SIZE, 0);", text)
     text = re.sub(r"asm\s+volatile\s*\((?:[^;]|\n)*?\)\s*;", ";", text)
     text = re.sub(r"^[ \t]*if \([^\n]*kA32Disabled\)+;[ \t]*\n", "", text, flags=re.M)
     return text

@@ -503,7 +503,14 @@ hipError_t hipSetDevice(int) { return hipSuccess; }
 hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int) {
     switch (a) {
         case hipDeviceAttributeWallClockRate: *v = 100000; break;
-        case hipDeviceAttributeMultiprocessorCount: *v = 256; break;
+        // SQEMU_CUS: a smaller emulated device, so that the grid-size rules
+        // (workgroups per CU) pick the large-grid kernels for small inputs
+        case hipDeviceAttributeMultiprocessorCount: {
+            const char* e = getenv("SQEMU_CUS");
+            *v = e ? atoi(e) : 256;
+            if (*v <= 0) *v = 256;
+            break;
+        }
         case hipDeviceAttributeMaxSharedMemoryPerBlock: *v = 160 * 1024; break;
         case hipDeviceAttributeCooperativeLaunch: *v = 1; break;
         default: return hipErrorInvalidValue;

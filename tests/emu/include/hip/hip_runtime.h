@@ -171,6 +171,14 @@ inline T shfl_xor(T v, int mask, int width) {
     return from_bits<T>(all[src]);
 }
 
+// global_load_lds_dword / _dwordx4 (a direct global -> LDS load): each lane
+// copies `size` bytes from its global address to the wavefront's LDS base +
+// offset + lane * size.  The copy happens at once; the device's wait for it
+// (s_waitcnt vmcnt) has nothing to wait for here.
+inline void global_load_lds(const void* src, void* lds, unsigned size, int offset) {
+    memcpy((char*)lds + offset + (size_t)g_lane * size, src, size);
+}
+
 inline int sdot4(int a, int b, int c, bool clamp) {
     (void)clamp;
     int s = c;
@@ -318,6 +326,13 @@ inline sqemu_v16f mfma_f32_32x32x8f16(sqemu_v4h a, sqemu_v4h b, sqemu_v16f c) {
 #define __builtin_amdgcn_wave_barrier() ::sqemu::wave_barrier()
 #define __builtin_amdgcn_update_dpp(o, s, c, r, b, bc) ::sqemu::update_dpp((o), (s), (c), (r), (b), (bc))
 #define __builtin_amdgcn_readlane(v, l) ::sqemu::readlane((v), (l))
+#define __builtin_amdgcn_s_barrier() ::sqemu::syncthreads()
+// the kernels take v_readfirstlane of wavefront-uniform values only
+#define __builtin_amdgcn_readfirstlane(v) (v)
+// wait counts have nothing to wait for: memory operations complete at once
+#define __builtin_amdgcn_s_waitcnt(n) ((void)(n))
+#define __builtin_amdgcn_global_load_lds(src, lds, size, off, aux) \
+    ::sqemu::global_load_lds((const void*)(src), (void*)(lds), (size), (off))
 // scheduling hints have no effect on the emulated execution
 #define __builtin_amdgcn_sched_barrier(m) ((void)(m))
 // v_exp_f32 (2^x): the host exp2f stands in for the device instruction

@@ -175,6 +175,21 @@ def test_long_prefill_full_rate_tiles_in_bounds(emu, models, wtype, tile):
     assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
 
 
+@pytest.mark.parametrize("unfused", ["0", "1"])
+def test_long_prefill_fused_epilogues_in_bounds(emu, models, unfused):
+    """A 140-row prefill on an emulated 8-CU device (SQEMU_CUS=8), so that the
+    grid-size rules pick the direct-to-LDS kernel's 128 x 128 tiles for the
+    FFN gate/up projection and its 128 x 64 tiles for the q|k|v projection:
+    with the fused epilogues (SiLU * up with its Q8_0 blocks; RoPE and the
+    KV-cache append) and without them (SQUIRREL_PREFILL_UNFUSED=1), every
+    access stays in bounds and the logits and quantization sites match the
+    oracle."""
+    steps, out = run(emu, [models["Q8_0"], W8A8, MULTI_KERNEL, 140, 1, 1, 160],
+                     env={"SQEMU_CUS": "8", "SQUIRREL_PREFILL_UNFUSED": unfused})
+    assert len(steps) == 2 and all(rel <= 1e-6 and dev == ora for _, rel, _, dev, ora in steps), out
+    assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
+
+
 @pytest.mark.parametrize("step,layer,site,element,kind", [
     (0, 0, 0, 100, 0),   # prefill, attention-norm output, one element
     (0, 1, 3, 700, 1),   # prefill, FFN activation, one block scale

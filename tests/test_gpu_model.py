@@ -684,6 +684,34 @@ def test_full_width_long_context_decode(model_dir):
 
 
 @FULL
+def test_long_prompt_fused_epilogues_bit_exact(model_dir, monkeypatch):
+    """1B widths (2 layers), Q8_0, a 2048-token prompt: the gate/up projection
+    (128 x 128 tiles) forms SiLU * up and its Q8_0 blocks in its epilogue, the
+    q|k|v projection (128 x 64 tiles) applies RoPE and appends to the KV
+    cache.  With the fusions off (SQUIRREL_PREFILL_UNFUSED=1: the same matmul
+    kernels, then the separate SiLU and RoPE kernels) the prefill and the
+    decode steps after it give the same logits bit for bit; so do the
+    register-staged matmul kernels (SQUIRREL_GEMM_DMA=0, which also turns the
+    fusions off)."""
+    from sqhip import ops
+    path = full_model(model_dir, "Q8_0", n_layers=2)
+    seq = full_seq(2048, 2, 6)
+    ops.gemm_counters(reset=True)
+    fused, toks_f, _ = run_gpu(path, seq, max_pos=2056, taps=False)
+    n = ops.gemm_counters(reset=True)
+    assert n["tile128_launches"] == 2 and n["tile128x64_launches"] == 6 and n["split_launches"] == 0, n
+    monkeypatch.setenv("SQUIRREL_PREFILL_UNFUSED", "1")
+    plain, toks_p, _ = run_gpu(path, seq, max_pos=2056, taps=False)
+    monkeypatch.delenv("SQUIRREL_PREFILL_UNFUSED")
+    monkeypatch.setenv("SQUIRREL_GEMM_DMA", "0")
+    staged, toks_s, _ = run_gpu(path, seq, max_pos=2056, taps=False)
+    assert toks_f == toks_p == toks_s
+    for step, (a, b, c) in enumerate(zip(fused, plain, staged)):
+        assert np.array_equal(a, b), f"step {step}: the fused and the separate forms differ"
+        assert np.array_equal(a, c), f"step {step}: the direct-to-LDS and register-staged kernels differ"
+
+
+@FULL
 def test_full_width_prefill_2048(model_dir):
     """1B widths (2 layers): a 2048-token batched prefill -- every matmul on
     the full-rate matrix-core kernel without a K split: per layer the gate/up
