@@ -619,18 +619,16 @@ struct RowsEpi {
 // matrix instructions folding the same per-block terms in the same order
 // (so both give the same bits), but its tiles never pass through registers:
 // global_load_lds_dwordx4 writes each 64-lane load (1 KB) straight into one
-// of ST LDS stages, and the loads run ST - 1 chunks ahead of the chunk being
-// multiplied.  Without staging registers the kernel fits three workgroups per
-// CU.  A stage holds, for one chunk of two blocks (64 bytes of K per row), the
-// BM activation rows and BN weight rows (Q8_0 payload) and one 32-bit word of
-// the two blocks' fp16 scales per row.  Row r's four 16-byte units are stored
-// with unit u at position u ^ ((r >> 1) & 3): the 16-byte operand reads of
-// eight consecutive rows at one unit then fall in distinct banks.  Each stage
-// is its own LDS object, so the compiler's wait before reading one stage
-// does not wait for the loads still in flight into the others; a bare
-// s_barrier (no fence, which would wait for every load in flight) follows
-// each wavefront's own wait for the stage's loads.  Needs an even block
-// count per K range (K a multiple of 64).
+// of ST LDS stages, and the loads run ST - 1 stages ahead of the one being
+// multiplied.  A stage holds, for SKB blocks of K (32 SKB bytes per row), the
+// BM activation rows and BN weight rows (Q8_0 payload) and the blocks' fp16
+// scales, two per 32-bit word: word d of row r at sa[d][r] (sw[d][r]).  Row
+// r's 16-byte units are stored with unit u at position u ^ dma_swz(r): the
+// 16-byte operand reads of 8 (16) consecutive rows at one unit then fall in
+// distinct banks of a 32 (64) bank LDS.  The loads are issued from inline
+// assembly (dma_to_lds), and each wavefront waits for its own loads of a
+// stage before a bare s_barrier (no fence: a fence would wait for every load
+// in flight).  Needs a block count per K range that is a multiple of SKB.
 //
 // Epilogues: RW_GATEUP (128 x 128 tiles) takes the stacked [gate; up]
 // matrix with column tile x holding gate rows 64 x + 32 h .. + 31 and the
@@ -643,31 +641,42 @@ struct RowsEpi {
 // lane l ^ 1) and appends the K and V rows to the cache, as rope_kv_kernel
 // does.  The same operations on the same values as the separate kernels, so
 // the same bits.
-template <int BM, int BN>
+typedef __attribute__((address_space(3))) int8_t lds_i8;
+
+template <int BM, int BN, int SKB>
 struct DmaStage {
-    int8_t a[BM * M8_KC];
-    int8_t w[BN * M8_KC];
-    uint32_t sa[BM];  // sa_b0 | sa_b1 << 16
-    uint32_t sw[BN];
+    int8_t a[BM * 32 * SKB];
+    int8_t w[BN * 32 * SKB];
+    uint32_t sa[SKB / 2][BM];  // sa_{2d} | sa_{2d+1} << 16
+    uint32_t sw[SKB / 2][BN];
 };
 
-__device__ __forceinline__ int dma_swz(int r) { return (r >> 1) & 3; }
+template <int SKB>
+__device__ __forceinline__ int dma_swz(int r) {
+    // (bits 0-3 of r only: the operand reads' row bases are multiples of 32)
+    if constexpr (SKB == 2) return ((r >> 1) ^ (r >> 2)) & 3;  // four units per row
+    else return (r ^ ((r >> 3) & 1)) & 7;                      // eight units per row
+}
 
 // A direct global -> LDS load (global_load_lds_dwordx4 for 16 bytes per lane,
-// global_load_lds_dword for 4): lane l's bytes land at lds + SIZE * l (lds is
-// the same on every lane: it goes to M0).  Issued from inline assembly, so
-// the compiler's wait-count pass does not see it: that pass cannot tell
-// which stage such a load writes once a loop merges its state, and would
-// make every read of any stage wait for every load in flight.  The caller
-// waits for the loads itself (s_waitcnt vmcnt) before a barrier.
+// global_load_lds_dword for 4): lane l reads `base + off` (base the same on
+// every lane, in SGPRs) and its bytes land at lds + SIZE * l (lds the same on
+// every lane: it goes to M0).  Issued from inline assembly, so the compiler's
+// wait-count pass does not see it: that pass cannot tell which stage such a
+// load writes once a loop merges its state, and would make every read of any
+// stage wait for every load in flight.  The caller waits for the loads itself
+// (s_waitcnt vmcnt) before a barrier.  M0 is named as clobbered; the
+// compiler sets M0 itself before each instruction of its own that reads it.
 template <int SIZE>
-__device__ __forceinline__ void dma_to_lds(const void* src, const void* lds) {
+__device__ __forceinline__ void dma_to_lds(const void* base, uint32_t off, lds_i8* lds) {
     static_assert(SIZE == 4 || SIZE == 16, "dword or dwordx4");
-    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) const void*)lds);
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds);
     if constexpr (SIZE == 16)
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
+                     : "memory", "m0");
     else
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
+                     : "memory", "m0");
 }
 
 // s_waitcnt immediate: at most n vector-memory operations outstanding (the
@@ -681,25 +690,42 @@ bool gemm_dma_enabled() {
     return !(e && !strcmp(e, "0"));
 }
 
-template <int BM, int BN, int ST>
-constexpr int dma_occupancy() { return BN == 128 ? 2 : 3; }
-constexpr int DMA_STAGES = 3;
+constexpr int DMA_KB = 2;      // blocks per stage
+constexpr int DMA_STAGES = 3;  // LDS stages
+// Wavefronts per SIMD: three on both tilings.  The 128 x 128 tiles get there
+// (at most 168 registers) by issuing each tile's matrix instructions right
+// before their combine instead of one tile ahead: the third wavefront hides
+// the matrix latency (193 against 210 us for the gate/up projection of a
+// 2048-token prompt, where two wavefronts with the one-ahead issue fit).
+// The 128 x 64 tiles keep the one-ahead issue (132 registers; four
+// wavefronts would spill).
+template <int BM, int BN>
+constexpr int dma_occupancy() { return 3; }
+// the loads' 32-bit byte offsets (row * k) stay below 2^31
+bool dma_offsets_fit(const MatView& w, int m) {
+    return (int64_t)max(w.rows, m) * w.k < ((int64_t)1 << 31);
+}
 
-template <int BM, int BN, int ST, int EPI>
-__global__ __launch_bounds__(256, (dma_occupancy<BM, BN, ST>())) void gemm_dma_kernel(
+template <int BM, int BN, int ST, int SKB, int EPI>
+__global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kernel(
     MatView w, const int8_t* __restrict__ aq, const uint16_t* __restrict__ ad, int m_rows,
     float* __restrict__ out, int ldo, int accumulate, int kbs, size_t split_stride, RowsEpi ep) {
     static_assert(BM == 128 && (BN == 64 || BN == 128), "tiles of 128 x 128 or 128 x 64");
     static_assert(EPI != RW_GATEUP || BN == 128, "the gate/up epilogue takes 128 x 128 tiles");
     static_assert(EPI != RW_QKV || BN == 64, "the q|k|v epilogue takes 128 x 64 tiles");
     static_assert(ST >= 2 && ST <= 4, "two to four stages");
+    static_assert(SKB == 2 || SKB == 4, "two or four blocks per stage");
     constexpr int SM = BM / 64, SN = BN / 64;
     constexpr int NT = SM * SN;
-    constexpr int LA = BM / 64, LW = BN / 64;  // 1 KB payload loads per wavefront and stage
-    constexpr int LPW = LA + LW + 1;           // loads per wavefront and stage (one scale load)
-    __shared__ __attribute__((aligned(16))) DmaStage<BM, BN> st0, st1, st2, st3;
+    constexpr int SKC = 32 * SKB, UPR = 2 * SKB;  // bytes and 16-byte units per row and stage
+    constexpr int LA = BM * UPR / 256, LW = BN * UPR / 256;  // 1 KB payload loads per wavefront and stage
+    constexpr int LS = SKB / 2;  // scale loads per wavefront and stage
+    constexpr int LPW = LA + LW + LS;
+    typedef DmaStage<BM, BN, SKB> Stage;
+    __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = w.k, KB = K >> 5;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int kb_begin = blockIdx.z * kbs, kb_end = min(KB, kb_begin + kbs);
@@ -707,44 +733,54 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN, ST>())) void gemm_dma_k
     const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
     const int fr = lane & 31, fh = lane >> 5;
 
-    // Per-lane source offsets of this wavefront's loads, at block 0.  Load q
-    // of a stage's payload covers rows 16 q .. 16 q + 15; lane j writes unit
-    // j % 4 of row 16 q + j / 4, which holds logical unit (j % 4) ^ swz(row).
-    size_t offa[LA], offw[LW];
+    // Per-lane byte offsets of this wavefront's loads from the stage's first
+    // block.  Payload load q covers 1 KB of the stage: rows 1024 q / SKC ..,
+    // lane j writing physical unit j % UPR of row 1024 q / SKC + j / UPR,
+    // which holds logical unit (j % UPR) ^ swz(row).
+    const int ffn = w.rows / 2;  // RW_GATEUP: FFN width
+    auto wrow_of = [&](int r) {  // weight row of tile row r
+        if constexpr (EPI == RW_GATEUP)
+            return ((r >> 5) & 1) * ffn + min(64 * (int)blockIdx.x + 32 * (r >> 6) + (r & 31), ffn - 1);
+        else
+            return min(n0 + r, w.rows - 1);
+    };
+    uint32_t offa[LA], offw[LW];
 #pragma unroll
     for (int i = 0; i < LA; i++) {
-        const int q = wave + 4 * i, r = 16 * q + (lane >> 2), u = (lane & 3) ^ dma_swz(r);
-        offa[i] = (size_t)min(m0 + r, m_rows - 1) * K + 16 * u;
+        const int q = wave + 4 * i, r = q * (1024 / SKC) + lane / UPR, u = (lane % UPR) ^ dma_swz<SKB>(r);
+        offa[i] = (uint32_t)(min(m0 + r, m_rows - 1) * K + 16 * u);
     }
-    const int ffn = w.rows / 2;  // RW_GATEUP: FFN width
 #pragma unroll
     for (int i = 0; i < LW; i++) {
-        const int q = wave + 4 * i, r = 16 * q + (lane >> 2), u = (lane & 3) ^ dma_swz(r);
-        int row = min(n0 + r, w.rows - 1);
-        if constexpr (EPI == RW_GATEUP)
-            row = ((r >> 5) & 1) * ffn + min(64 * (int)blockIdx.x + 32 * (r >> 6) + (r & 31), ffn - 1);
-        offw[i] = (size_t)row * K + 16 * u;
+        const int q = wave + 4 * i, r = q * (1024 / SKC) + lane / UPR, u = (lane % UPR) ^ dma_swz<SKB>(r);
+        offw[i] = (uint32_t)(wrow_of(r) * K + 16 * u);
     }
-    // The scale words: waves 0 and 1 take the activation rows 64 v .. 64 v +
-    // 63; waves 2 and 3 the weight rows (with 64 columns, 32 rows each, on
-    // lanes 0-31).
+    // The scale words: wavefronts 0 and 1 take the activation rows 64 v ..
+    // 64 v + 63, wavefronts 2 and 3 the weight rows (with 64 columns, 32 rows
+    // each, on lanes 0-31); load d of a stage is word d of every row.
     const bool sc_act = wave < 2;
     const int sc_row = sc_act ? 64 * wave + lane : (BN == 128 ? 64 * (wave - 2) + lane : 32 * (wave - 2) + lane);
     const bool sc_on = sc_act || BN == 128 || lane < 32;
-    int sc_wrow = min(n0 + sc_row, w.rows - 1);
-    if constexpr (EPI == RW_GATEUP)
-        sc_wrow = ((sc_row >> 5) & 1) * ffn + min(64 * (int)blockIdx.x + 32 * (sc_row >> 6) + (sc_row & 31), ffn - 1);
-    const size_t offs = sc_act ? (size_t)min(m0 + sc_row, m_rows - 1) * KB : (size_t)sc_wrow * KB;
+    const uint32_t offs = 2 * (uint32_t)((sc_act ? min(m0 + sc_row, m_rows - 1) : wrow_of(sc_row)) * KB);
     const uint16_t* sc_src = sc_act ? ad : w.scale;
     const int sc_dst = sc_act ? 64 * wave : (BN == 128 ? 64 * (wave - 2) : 32 * (wave - 2));
 
-    auto issue = [&](DmaStage<BM, BN>& S, int kb0) {
+    auto lds = [](Stage& S) { return (lds_i8*)(int8_t*)&S; };
+    auto issue = [&](Stage& S, int kb0) {
+        lds_i8* const base = lds(S);
+        const int8_t* ga = aq + (size_t)kb0 * 32;
+        const int8_t* gw = (const int8_t*)w.qs + (size_t)kb0 * 32;
 #pragma unroll
-        for (int i = 0; i < LA; i++) dma_to_lds<16>(aq + offa[i] + (size_t)kb0 * 32, S.a + 1024 * (wave + 4 * i));
+        for (int i = 0; i < LA; i++) dma_to_lds<16>(ga, offa[i], base + 1024 * (wave + 4 * i));
 #pragma unroll
-        for (int i = 0; i < LW; i++)
-            dma_to_lds<16>((const int8_t*)w.qs + offw[i] + (size_t)kb0 * 32, S.w + 1024 * (wave + 4 * i));
-        if (sc_on) dma_to_lds<4>(sc_src + offs + kb0, (sc_act ? S.sa : S.sw) + sc_dst);
+        for (int i = 0; i < LW; i++) dma_to_lds<16>(gw, offw[i], base + BM * SKC + 1024 * (wave + 4 * i));
+        if (sc_on) {
+            const uint16_t* gs = sc_src + kb0;
+            lds_i8* const sb = base + BM * SKC + BN * SKC + (sc_act ? 0 : 4 * LS * BM);
+#pragma unroll
+            for (int d = 0; d < LS; d++)
+                dma_to_lds<4>(gs + 2 * d, offs, sb + 4 * (d * (sc_act ? BM : BN) + sc_dst));
+        }
     };
 
     m8_v16f acc[NT];
@@ -753,70 +789,83 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN, ST>())) void gemm_dma_k
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
 
-    // Operand addresses within a stage (bytes), for block 0 and row tile i /
-    // column tile j; block 1 is unit 2 + fh, which XORs the same way.
-    int ra[SM], rw[SN];
+    // Operand addresses within a stage (bytes): row tile i / column tile j
+    // at block b is logical unit 2 b + fh (wm, wn and 32 i, 32 j are
+    // multiples of 32, so swz depends on fr alone).
+    int ra[SM], rw[SN], ua[SKB];
 #pragma unroll
-    for (int i = 0; i < SM; i++) {
-        const int r = wm + 32 * i + fr;
-        ra[i] = r * M8_KC;
-    }
+    for (int i = 0; i < SM; i++) ra[i] = (wm + 32 * i + fr) * SKC;
 #pragma unroll
-    for (int j = 0; j < SN; j++) {
-        const int r = wn + 32 * j + fr;
-        rw[j] = r * M8_KC;
-    }
-    const int ua0 = 16 * (fh ^ dma_swz(fr)), ua1 = 16 * ((2 + fh) ^ dma_swz(fr));
+    for (int j = 0; j < SN; j++) rw[j] = (wn + 32 * j + fr) * SKC;
+#pragma unroll
+    for (int b = 0; b < SKB; b++) ua[b] = 16 * ((2 * b + fh) ^ dma_swz<SKB>(fr));
     const uint32_t lo_mask = fh ? 0u : 0xFFFFFFFFu;  // k-slots 4-7 (lanes 32-63) are zero
-    // (wm, wn and 32 i, 32 j are multiples of 8, so swz depends on fr alone)
 
-    auto compute = [&](const DmaStage<BM, BN>& S) {
+    auto compute = [&](const Stage& S) {
         // scale operands: lanes 0-31 hold k-slots 0-3 of row (column) fr, the
-        // others slots 4-7 (zero).  Block 0 pairs (sa_b0, 0) with (sw_b0,
-        // sw_b1); block 1 pairs (0, sa_b1) with the same.
-        uint32_t sar[SM], swr[SN];
+        // others slots 4-7 (zero).  Block 2 d pairs (sa_{2d}, 0) with (sw_{2d},
+        // sw_{2d+1}); block 2 d + 1 pairs (0, sa_{2d+1}) with the same.
+        uint32_t sar[LS][SM], swr[LS][SN];
 #pragma unroll
-        for (int i = 0; i < SM; i++) sar[i] = S.sa[wm + 32 * i + fr] & lo_mask;
+        for (int d = 0; d < LS; d++) {
 #pragma unroll
-        for (int j = 0; j < SN; j++) swr[j] = S.sw[wn + 32 * j + fr] & lo_mask;
+            for (int i = 0; i < SM; i++) sar[d][i] = S.sa[d][wm + 32 * i + fr] & lo_mask;
+#pragma unroll
+            for (int j = 0; j < SN; j++) swr[d][j] = S.sw[d][wn + 32 * j + fr] & lo_mask;
+        }
         sq_v4i af[SM], bf[SN];
         auto operands = [&](int b) {
-            const int ua = b ? ua1 : ua0;
 #pragma unroll
-            for (int i = 0; i < SM; i++) af[i] = *(const sq_v4i*)(S.a + ra[i] + ua);
+            for (int i = 0; i < SM; i++) af[i] = *(const sq_v4i*)(S.a + ra[i] + ua[b]);
 #pragma unroll
-            for (int j = 0; j < SN; j++) bf[j] = *(const sq_v4i*)(S.w + rw[j] + ua);
+            for (int j = 0; j < SN; j++) bf[j] = *(const sq_v4i*)(S.w + rw[j] + ua[b]);
         };
         auto sa_op = [&](int b, int i) {
-            const uint32_t v = b ? (sar[i] & 0xFFFF0000u) : (sar[i] & 0xFFFFu);
+            const uint32_t v = (b & 1) ? (sar[b >> 1][i] & 0xFFFF0000u) : (sar[b >> 1][i] & 0xFFFFu);
             return __builtin_bit_cast(mq_v4h, make_uint2(v, 0u));
         };
-        auto sw_op = [&](int j) { return __builtin_bit_cast(mq_v4h, make_uint2(swr[j], 0u)); };
+        auto sw_op = [&](int b, int j) { return __builtin_bit_cast(mq_v4h, make_uint2(swr[b >> 1][j], 0u)); };
         const m8_v16i izero = {};
         const m8_v16f fzero = {};
-        m8_v16i d[2];
-        m8_v16f sc[2];
-        operands(0);
-        d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0], bf[0], izero, 0, 0, 0);
-        sc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa_op(0, 0), sw_op(0), fzero, 0, 0, 0);
+        if constexpr (BN == 128) {
+            // (block, tile) pairs k = NT b + t in order, each pair's matrix
+            // instructions right before its combine
 #pragma unroll
-        for (int k = 0; k < NT * M8_KB; k++) {
-            if (k + 1 < NT * M8_KB) {
-                const int t1 = (k + 1) % NT, i = t1 / SN, j = t1 % SN, b1 = (k + 1) / NT;
-                if (t1 == 0) operands(b1);
-                d[(k + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], izero, 0, 0, 0);
-                sc[(k + 1) & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa_op(b1, i), sw_op(j), fzero, 0, 0, 0);
+            for (int k = 0; k < NT * SKB; k++) {
+                const int t = k % NT, i = t / SN, j = t % SN, b = k / NT;
+                if (t == 0) operands(b);
+                const m8_v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], izero, 0, 0, 0);
+                const m8_v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa_op(b, i), sw_op(b, j), fzero, 0, 0, 0);
+                // the combine of the reference's aarch64 kernels (dot_prod.rs:189-252):
+                // acc = fma(f32(isum), sa * sw, acc)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[t][r] = fmaf((float)d[r], sc[r], acc[t][r]);
             }
-            if constexpr (BN == 128) __builtin_amdgcn_sched_barrier(0);
-            const int t = k % NT;
+        } else {
+            // the same pairs, each one's matrix instructions issued one pair
+            // ahead of its combine
+            m8_v16i d[2];
+            m8_v16f sc[2];
+            operands(0);
+            d[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0], bf[0], izero, 0, 0, 0);
+            sc[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa_op(0, 0), sw_op(0, 0), fzero, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[t][r] = fmaf((float)d[k & 1][r], sc[k & 1][r], acc[t][r]);
-            if constexpr (BN == 128) __builtin_amdgcn_sched_barrier(0);
+            for (int k = 0; k < NT * SKB; k++) {
+                if (k + 1 < NT * SKB) {
+                    const int t1 = (k + 1) % NT, i = t1 / SN, j = t1 % SN, b1 = (k + 1) / NT;
+                    if (t1 == 0) operands(b1);
+                    d[(k + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], izero, 0, 0, 0);
+                    sc[(k + 1) & 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa_op(b1, i), sw_op(b1, j), fzero, 0, 0, 0);
+                }
+                const int t = k % NT;
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[t][r] = fmaf((float)d[k & 1][r], sc[k & 1][r], acc[t][r]);
+            }
         }
     };
 
-    // Wait until this wavefront's loads of the chunk about to be multiplied
-    // have landed: `ahead` later chunks' loads may stay in flight.
+    // Wait until this wavefront's loads of the stage about to be multiplied
+    // have landed: `ahead` later stages' loads may stay in flight.
     auto wait_stage = [&](int ahead) {
         if (ahead >= 2) __builtin_amdgcn_s_waitcnt(dma_vmcnt(2 * LPW));
         else if (ahead == 1) __builtin_amdgcn_s_waitcnt(dma_vmcnt(LPW));
@@ -830,25 +879,23 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN, ST>())) void gemm_dma_k
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
-    // One chunk: wait for its stage, then refill the stage the previous chunk
-    // used and multiply this one.  Each call site names its LDS objects
-    // directly, so the compiler's wait before the stage's reads covers only
-    // that stage's loads.
-    const int n = (kb_end - kb_begin) / M8_KB;
-    auto chunk = [&](int cc, DmaStage<BM, BN>& cur, DmaStage<BM, BN>& refill) {
+    // One stage: wait for its loads, then refill the stage the previous one
+    // used and multiply this one.
+    const int n = (kb_end - kb_begin) / SKB;
+    auto chunk = [&](int cc, Stage& cur, Stage& refill) {
         if (cc < n) {
             wait_stage(min(ST - 2, n - 1 - cc));
             barrier();
-            if (cc + ST - 1 < n) issue(refill, kb_begin + M8_KB * (cc + ST - 1));
+            if (cc + ST - 1 < n) issue(refill, kb_begin + SKB * (cc + ST - 1));
             compute(cur);
         }
     };
-    // the first ST - 1 chunks' loads
+    // the first ST - 1 stages' loads
     if (0 < n) issue(st0, kb_begin);
     if constexpr (ST >= 3)
-        if (1 < n) issue(st1, kb_begin + M8_KB);
+        if (1 < n) issue(st1, kb_begin + SKB);
     if constexpr (ST >= 4)
-        if (2 < n) issue(st2, kb_begin + 2 * M8_KB);
+        if (2 < n) issue(st2, kb_begin + 2 * SKB);
     for (int c = 0; c < n; c += ST) {
         if constexpr (ST == 2) {
             chunk(c, st0, st1);
@@ -1250,12 +1297,13 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
     count_launch(splits, BN);
     // Q8_0 weights with an even block count take the direct-to-LDS kernel
     // (the same results); Q4_0 nibbles are expanded while staging.
-    const bool dma = WT == WT_Q8_0 && KB % 2 == 0 && gemm_dma_enabled();
+    const bool dma = WT == WT_Q8_0 && kbs % DMA_KB == 0 && KB % DMA_KB == 0 && dma_offsets_fit(w, m) &&
+                     gemm_dma_enabled();
     constexpr int ST = DMA_STAGES;
     hipError_t e;
     if (splits == 1) {
         if (dma)
-            hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, ST, RW_STORE>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m,
+            hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, ST, DMA_KB, RW_STORE>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m,
                                out, ldo, acc ? 1 : 0, KB, (size_t)0, RowsEpi{});
         else
             hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m, out, ldo,
@@ -1263,7 +1311,7 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
     } else {
         const size_t stride = (size_t)m * w.rows;
         if (dma)
-            hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, ST, RW_STORE>), dim3(gx, gy, splits), dim3(256), 0, s, w, aq,
+            hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, ST, DMA_KB, RW_STORE>), dim3(gx, gy, splits), dim3(256), 0, s, w, aq,
                                ad, m, ws, w.rows, 0, kbs, stride, RowsEpi{});
         else
             hipLaunchKernelGGL((gemm_mfma32_kernel<WT, BM, BN>), dim3(gx, gy, splits), dim3(256), 0, s, w, aq, ad, m,
@@ -1378,14 +1426,16 @@ template <int BN, int EPI>
 int run_dma_fused(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, int gx,
                   const RowsEpi& ep) {
     const int KB = w.k / 32, gy = (m + 127) / 128;
-    if (w.wtype != WT_Q8_0 || KB % 2 || !gemm_dma_enabled() || gemm_tile_override() != TILE_AUTO) return -1;
+    if (w.wtype != WT_Q8_0 || KB % DMA_KB || !dma_offsets_fit(w, m) || !gemm_dma_enabled() ||
+        gemm_tile_override() != TILE_AUTO)
+        return -1;
     if (gx * gy < 2 * device_cus()) return -1;
     // the unfused path's choice for this grid: 128 x 128 tiles where those
     // fill the device, else 128 x 64
     const int g128 = (w.rows + 127) / 128 * gy;
     if ((BN == 128) != (g128 >= 2 * device_cus())) return -1;
     count_launch(1, BN);
-    hipLaunchKernelGGL((gemm_dma_kernel<128, BN, DMA_STAGES, EPI>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m,
+    hipLaunchKernelGGL((gemm_dma_kernel<128, BN, DMA_STAGES, DMA_KB, EPI>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m,
                        nullptr, 0, 0, KB, (size_t)0, ep);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));

@@ -44,8 +44,8 @@ def rewrite(text: str) -> str:
                   r"\1* \2 = (\1*)::sqemu::dyn_lds();", text)
     # the direct-to-LDS load helper issues its load from inline assembly:
     # here the emulated load does the copy
-    text = re.sub(r"(void dma_to_lds\(const void\* src, const void\* lds\) \{)",
-                  r"\1\n    ::sqemu::global_load_lds(src, (void*)lds, SIZE, 0);", text)
+    text = re.sub(r"(void dma_to_lds\(const void\* base, uint32_t off, lds_i8\* lds\) \{)",
+                  r"\1\n    ::sqemu::global_load_lds((const char*)base + off, (void*)lds, SIZE, 0);", text)
     text = re.sub(r"asm\s+volatile\s*\((?:[^;]|\n)*?\)\s*;", ";", text)
     text = re.sub(r"^[ \t]*if \([^\n]*kA32Disabled\)+;[ \t]*\n", "", text, flags=re.M)
     return text
