@@ -1282,10 +1282,10 @@ int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
 // holds the partial tiles.
 template <int WT, int BM, int BN>
 int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
-               bool acc, float* ws, size_t ws_floats, bool force) {
+               bool acc, float* ws, size_t ws_floats, bool force, int target = 0) {
     const int gx = (w.rows + BN - 1) / BN, gy = (m + BM - 1) / BM;
     const int KB = w.k / 32, chunks = (KB + M8_KB - 1) / M8_KB;
-    const int full = 2 * device_cus();
+    const int full = target > 0 ? target : 2 * device_cus();
     if (!force && gx * gy < full) return 1;
     int splits = 1;
     if (ws != nullptr && gx * gy < full) {
@@ -1403,6 +1403,19 @@ int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_
     if (tile == TILE_128 || (tile == TILE_AUTO && m >= 128)) {
         const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128);
         if (st != 1) return st;
+    }
+    // A long K on too few 128 x 128 tiles (the FFN down projection of a
+    // 2048-token prompt: 256 tiles, K = 8192): split K so that the grid
+    // takes three workgroups per CU, one round, and sum the partials in
+    // split order (about half the time of the unsplit 128 x 64 tiles, whose
+    // 512 workgroups leave a third of the direct-to-LDS kernel's slots empty).
+    if (WT == WT_Q8_0 && tile == TILE_AUTO && m >= 128 && w.k / 32 >= 128 && ws != nullptr) {
+        const int cus = device_cus(), g = (w.rows + 127) / 128 * ((m + 127) / 128);
+        const int splits = (3 * cus + g - 1) / g;
+        if (g < 2 * cus && splits <= 4 && (size_t)splits * m * w.rows <= ws_floats) {
+            const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, true, 3 * cus);
+            if (st != 1) return st;
+        }
     }
     if (tile == TILE_128X64 || (tile == TILE_AUTO && m >= 128)) {
         const int st = run_mfma32<WT, 128, 64>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128X64);

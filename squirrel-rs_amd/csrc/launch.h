@@ -131,6 +131,9 @@ int launch_log_softmax_at(hipStream_t s, const float* logits, int n, const uint3
 // ws: room for ws_floats floats of partial tiles, for a K split of the
 // integer path when the output has few tiles (null: no split).
 constexpr size_t kGemmSplitFloats = (size_t)4 << 20;
+// The model context's K-split workspace: three partial 2048 x 2048 tiles
+// (the FFN down projection of a 2048-token prompt) and more.
+constexpr size_t kPrefillSplitFloats = (size_t)16 << 20;
 // Integer matmul launches on the matrix cores since the last reset: out[0]
 // all, [1] with a K split, [2] on 128 x 128 tiles, [3] the largest split.
 void gemm_counters(bool reset, uint64_t* out);

@@ -405,7 +405,7 @@ int ensure_prefill(sq_ctx* c, size_t n) {
         (st = dmalloc(&c->p_act, n * F)) || (st = dmalloc(&c->p_aq, n * wmax)) ||
         (st = dmalloc(&c->p_ad, n * wmax / 32)))
         return st;
-    if (!c->p_split && (st = dmalloc(&c->p_split, kGemmSplitFloats))) return st;
+    if (!c->p_split && (st = dmalloc(&c->p_split, kPrefillSplitFloats))) return st;
     c->cap_rows = n;
     return 0;
 }
@@ -650,7 +650,7 @@ int run_prefill(sq_ctx* c, size_t n) {
         if (fused_qkv > 0) return fused_qkv;
         if (fused_qkv != 0) {
             if ((st = launch_gemm(s, view(L.qkv), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_qkv,
-                                  QD + 2 * KVD, false, c->p_split, kGemmSplitFloats)) ||
+                                  QD + 2 * KVD, false, c->p_split, kPrefillSplitFloats)) ||
                 (st = phase(2)) ||
                 (st = launch_rope_kv_rows(s, c->p_qkv, QD + 2 * KVD, N, QD, KVD, hd, pos0, c->rope, c->p_q, kc, vc)))
                 return st;
@@ -667,7 +667,7 @@ int run_prefill(sq_ctx* c, size_t n) {
         if (a8 && (st = tap(l, 1, QD))) return st;
         if ((st = phase(0)) ||
             (st = launch_gemm(s, view(L.o), m->wtype, a8, c->p_aq, c->p_ad, c->p_attn, N, c->p_hidden, D, true,
-                              c->p_split, kGemmSplitFloats)) ||
+                              c->p_split, kPrefillSplitFloats)) ||
             (st = phase(2)))
             return st;
         if ((st = launch_rmsnorm_rows(s, c->p_hidden, L.ffn_norm, N, D, g.eps, a8 ? nullptr : c->p_normed,
@@ -695,7 +695,7 @@ int run_prefill(sq_ctx* c, size_t n) {
         }
         if (fused != 0) {
             if ((st = launch_gemm(s, view(L.gateup), m->wtype, a8, c->p_aq, c->p_ad, c->p_normed, N, c->p_gu, 2 * F,
-                                  false, c->p_split, kGemmSplitFloats)) ||
+                                  false, c->p_split, kPrefillSplitFloats)) ||
                 (st = phase(2)) ||
                 (st = launch_silu_mul_rows(s, c->p_gu, F, (size_t)N * F, a8 ? nullptr : c->p_act,
                                            a8 ? c->p_aq : nullptr, c->p_ad)))
@@ -706,7 +706,7 @@ int run_prefill(sq_ctx* c, size_t n) {
         if ((a8 && (st = tap(l, 3, F, fq, fd)))) return st;
         if ((st = phase(0)) ||
             (st = launch_gemm(s, view(L.down), m->wtype, a8, fq, fd, c->p_act, N, c->p_hidden, D, true,
-                              c->p_split, kGemmSplitFloats)) ||
+                              c->p_split, kPrefillSplitFloats)) ||
             (st = phase(2)))
             return st;
     }

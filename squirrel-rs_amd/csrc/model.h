@@ -117,7 +117,7 @@ struct sq_ctx {
     float* p_act = nullptr;
     int8_t* p_aq = nullptr;
     uint16_t* p_ad = nullptr;
-    float* p_split = nullptr;  // partial tiles of a K-split prefill matmul (kGemmSplitFloats)
+    float* p_split = nullptr;  // partial tiles of a K-split prefill matmul (kPrefillSplitFloats)
 
     // persistent decode step (one launch per token)
     bool persist = false;
