@@ -722,7 +722,8 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kerne
     constexpr int LS = SKB / 2;  // scale loads per wavefront and stage
     constexpr int LPW = LA + LW + LS;
     typedef DmaStage<BM, BN, SKB> Stage;
-    __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
+    __shared__ __attribute__((aligned(16))) Stage stg[ST];
+    Stage &st0 = stg[0], &st1 = stg[1 % ST], &st2 = stg[2 % ST], &st3 = stg[3 % ST];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -914,23 +915,58 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kerne
     // element r of tile t is row 8 (r / 4) + 4 fh + r % 4 of row tile t / SN,
     // column fr of column tile t % SN
     if constexpr (EPI == RW_GATEUP) {
-        const int f = 64 * blockIdx.x + 32 * (wave & 1) + fr;  // FFN column
+        // SiLU(gate) * up of the workgroup's 128 rows x 64 FFN columns goes
+        // to LDS (the stages are free once every wavefront is past its last
+        // chunk); then thread t takes row t / 2, block t % 2: the block's
+        // maximum, Q8_0 scale and quants as silu_mul8_kernel forms them,
+        // stored as 32 bytes.  Row r's 16-byte chunk c (of 16) sits at
+        // position c of its half rotated by 2 r + c / 8, so a row's writes and
+        // the readers' 16-byte reads of 8 consecutive threads fall in distinct
+        // banks (of 32).
+        static_assert(BM * 64 * sizeof(float) <= sizeof(stg), "the SiLU tile fits the stages");
+        float* const tileb = (float*)&stg[0];
+        auto at = [](int row, int col) {
+            const int c = col >> 2;
+            return row * 64 + 4 * ((c & 8) | (((c & 7) + 2 * row + (c >> 3)) & 7)) + (col & 3);
+        };
+        barrier();
+        const int fc = 32 * (wave & 1) + fr;  // the workgroup's FFN column
 #pragma unroll
         for (int i = 0; i < SM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const float g = acc[SN * i][r], u = acc[SN * i + 1][r];
-                const float v = (g * sq_sigmoid(g)) * u;  // silu(gate) * up (silu_mul8_kernel)
-                float mx = fabsf(v);
-#pragma unroll
-                for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-                const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), inv = sq_q8_inv(scale);
-                const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
-                if (m < m_rows && f < ffn) {
-                    ep.act_q[(size_t)m * ffn + f] = sq_q8_quant(v, inv);
-                    if (fr == 0) ep.act_d[(size_t)m * (ffn / 32) + f / 32] = sq_f32_to_f16(scale);
-                }
+                const int row = wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
+                tileb[at(row, fc)] = (g * sq_sigmoid(g)) * u;  // silu(gate) * up (silu_mul8_kernel)
             }
+        barrier();
+        const int row = tid >> 1, blk = tid & 1, m = m0 + row, f0 = 64 * blockIdx.x + 32 * blk;
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const sq_v4f x = *(const sq_v4f*)(tileb + at(row, 32 * blk + 4 * k));
+            v[4 * k] = x.x;
+            v[4 * k + 1] = x.y;
+            v[4 * k + 2] = x.z;
+            v[4 * k + 3] = x.w;
+        }
+        float mx = fabsf(v[0]);
+#pragma unroll
+        for (int k = 1; k < 32; k++) mx = fmaxf(mx, fabsf(v[k]));
+        const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), inv = sq_q8_inv(scale);
+        if (m < m_rows && f0 < ffn) {
+            unsigned q[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                q[k] = 0;
+#pragma unroll
+                for (int c = 0; c < 4; c++) q[k] |= (unsigned)(uint8_t)sq_q8_quant(v[4 * k + c], inv) << (8 * c);
+            }
+            sq_v4i* const dst = (sq_v4i*)(ep.act_q + (size_t)m * ffn + f0);
+            dst[0] = sq_v4i{(int)q[0], (int)q[1], (int)q[2], (int)q[3]};
+            dst[1] = sq_v4i{(int)q[4], (int)q[5], (int)q[6], (int)q[7]};
+            ep.act_d[(size_t)m * (ffn / 32) + f0 / 32] = sq_f32_to_f16(scale);
+        }
         return;
     }
     if constexpr (EPI == RW_QKV) {
