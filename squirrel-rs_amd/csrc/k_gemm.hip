@@ -874,7 +874,9 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kerne
     };
     // (every LDS read of a stage is consumed by a matrix instruction before
     // the wavefront reaches the next barrier, so no read is still in flight
-    // when another wavefront's loads overwrite the stage)
+    // when another wavefront's loads overwrite the stage; the bare barrier
+    // does not wait for LDS writes, so it serves the main loop only, which
+    // writes LDS through the loads alone)
     auto barrier = [] {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -923,13 +925,16 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kerne
         // position c of its half rotated by 2 r + c / 8, so a row's writes and
         // the readers' 16-byte reads of 8 consecutive threads fall in distinct
         // banks (of 32).
+        // The two barriers here are __syncthreads: each wavefront's LDS
+        // writes must have landed before another reads them (the main loop's
+        // bare barrier waits for nothing, and no load is in flight by now).
         static_assert(BM * 64 * sizeof(float) <= sizeof(stg), "the SiLU tile fits the stages");
         float* const tileb = (float*)&stg[0];
         auto at = [](int row, int col) {
             const int c = col >> 2;
             return row * 64 + 4 * ((c & 8) | (((c & 7) + 2 * row + (c >> 3)) & 7)) + (col & 3);
         };
-        barrier();
+        __syncthreads();
         const int fc = 32 * (wave & 1) + fr;  // the workgroup's FFN column
 #pragma unroll
         for (int i = 0; i < SM; i++)
@@ -939,7 +944,7 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kerne
                 const int row = wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
                 tileb[at(row, fc)] = (g * sq_sigmoid(g)) * u;  // silu(gate) * up (silu_mul8_kernel)
             }
-        barrier();
+        __syncthreads();
         const int row = tid >> 1, blk = tid & 1, m = m0 + row, f0 = 64 * blockIdx.x + 32 * blk;
         float v[32];
 #pragma unroll
