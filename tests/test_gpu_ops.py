@@ -155,6 +155,33 @@ def test_linear_matches_oracle(wtype, k, n, m, f32_acts):
     assert np.all(err <= 4e-6 * mag + 1e-6), float((err / (mag + 1e-30)).max())
 
 
+@pytest.mark.parametrize("k", [2048, 8192])
+@pytest.mark.parametrize("tile", ["128x64", "128"])
+def test_direct_to_lds_matmul_matches_register_staged(tile, k, monkeypatch):
+    """Q8_0 weights on ragged tiles (1000 prompt rows: 7 full 128-row tiles
+    and 104 rows; 4000 columns: 31 full 128-column tiles and 32): the
+    direct-to-LDS kernel (three LDS stages, swizzled rows, loads issued from
+    assembly) and the register-staged kernel (SQUIRREL_GEMM_DMA=0) fold the
+    same per-block terms in the same order, so they agree bit for bit."""
+    m, n = 1000, 4000
+    w, _ = quant_weights(O.Q8_0, n, k, seed=91)
+    x = (rng(5).standard_normal((m, k)) * 1.5).astype(np.float32)
+    W = ops.Weight(O.Q8_0, w, n, k)
+    d_x = DeviceArray.from_numpy(x)
+    monkeypatch.setenv("SQUIRREL_GEMM_TILE", tile)
+    outs = {}
+    for dma in ("1", "0"):
+        monkeypatch.setenv("SQUIRREL_GEMM_DMA", dma)
+        out = DeviceArray((m, n))
+        ops.gemm_counters(reset=True)
+        ops.linear(d_x, W, out)
+        got = ops.gemm_counters(reset=True)
+        assert got["launches"] == 1 and got["split_launches"] == 0, got
+        outs[dma] = out.numpy()
+    assert np.array_equal(outs["1"], outs["0"])
+    assert np.all(np.isfinite(outs["1"]))
+
+
 @pytest.mark.parametrize("wtype", [O.Q8_0, O.Q4_0])
 def test_matmul_tiles_agree(wtype, monkeypatch):
     """The prefill matmul's three tilings (64 x 64 on v_mfma_i32_16x16x32_i8,
