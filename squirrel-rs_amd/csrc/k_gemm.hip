@@ -1026,6 +1026,45 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
     *o = accumulate ? *o + v : v;
 }
 
+// The same sums four elements per thread (16-byte loads and stores) where
+// n, ldo and stride are multiples of 4 and the buffers 16-byte aligned.
+__global__ __launch_bounds__(256) void split_sum4_kernel(const float* __restrict__ ws, int splits, size_t stride,
+                                                         int m, int n, float* __restrict__ out, int ldo,
+                                                         int accumulate) {
+    const size_t i = 4 * ((size_t)blockIdx.x * 256 + threadIdx.x);
+    if (i >= (size_t)m * n) return;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int z = 0; z < splits; z++) {
+        const float4 p = *(const float4*)(ws + z * stride + i);
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+    }
+    float4* o = (float4*)(out + (i / n) * (size_t)ldo + i % n);
+    if (accumulate) {
+        const float4 a = *o;
+        v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+    }
+    *o = v;
+}
+
+// out (+)= the split partials in split order, on the vector kernel where the
+// shapes and buffers allow it.
+int launch_split_sum(hipStream_t s, const float* ws, int splits, size_t stride, int m, int n, float* out, int ldo,
+                     bool acc) {
+    const size_t total = (size_t)m * n;
+    if (n % 4 == 0 && ldo % 4 == 0 && stride % 4 == 0 && (((uintptr_t)ws | (uintptr_t)out) & 15) == 0)
+        hipLaunchKernelGGL(split_sum4_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, s, ws, splits,
+                           stride, m, n, out, ldo, acc ? 1 : 0);
+    else
+        hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws, splits,
+                           stride, m, n, out, ldo, acc ? 1 : 0);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("split sum launch: ") + hipGetErrorString(e));
+    return 0;
+}
+
 // ---- few activation rows: the weights streamed once --------------------------
 // A prompt of a few dozen rows (the short prompts of a generation) makes the
 // matmul a weight stream with little arithmetic per byte.  The 64 x 64
@@ -1303,8 +1342,7 @@ int run_mfma(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* 
                            kbs, stride);
         e = hipGetLastError();
         if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
-        hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
-                           m, w.rows, out, ldo, acc ? 1 : 0);
+        if (const int st = launch_split_sum(s, ws, splits, stride, m, w.rows, out, ldo, acc)) return st;
     }
     e = hipGetLastError();
     if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
@@ -1359,8 +1397,7 @@ int run_mfma32(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t
                                ws, w.rows, 0, kbs, stride);
         e = hipGetLastError();
         if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
-        hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
-                           m, w.rows, out, ldo, acc ? 1 : 0);
+        if (const int st = launch_split_sum(s, ws, splits, stride, m, w.rows, out, ldo, acc)) return st;
     }
     e = hipGetLastError();
     if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
@@ -1388,8 +1425,7 @@ int launch_rows(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_
                            ad, m, ws, w.rows, 0, per, kbs, stride, RowsEpi{});
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
-        hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)((stride + 255) / 256)), dim3(256), 0, s, ws, splits, stride,
-                           m, w.rows, out, ldo, acc ? 1 : 0);
+        if (const int st = launch_split_sum(s, ws, splits, stride, m, w.rows, out, ldo, acc)) return st;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
