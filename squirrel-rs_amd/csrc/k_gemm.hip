@@ -1481,15 +1481,16 @@ int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_
         const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128);
         if (st != 1) return st;
     }
-    // A long K on too few 128 x 128 tiles (the FFN down projection of a
-    // 2048-token prompt: 256 tiles, K = 8192): split K so that the grid
-    // takes three workgroups per CU, one round, and sum the partials in
-    // split order (about half the time of the unsplit 128 x 64 tiles, whose
-    // 512 workgroups leave a third of the direct-to-LDS kernel's slots empty).
-    if (WT == WT_Q8_0 && tile == TILE_AUTO && m >= 128 && w.k / 32 >= 128 && ws != nullptr) {
+    // About one 128 x 128 tile per CU (the o and FFN down projections of a
+    // 2048-token prompt: 256 tiles, K = 2048 and 8192): split K three ways,
+    // so that the grid takes three workgroups per CU, one round, and sum the
+    // partials in split order (about half the time of the unsplit 128 x 64
+    // tiles for the down projection, whose 512 workgroups leave a third of
+    // the direct-to-LDS kernel's slots empty).
+    if (WT == WT_Q8_0 && tile == TILE_AUTO && m >= 128 && w.k / 32 >= 64 && ws != nullptr) {
         const int cus = device_cus(), g = (w.rows + 127) / 128 * ((m + 127) / 128);
         const int splits = (3 * cus + g - 1) / g;
-        if (g < 2 * cus && splits <= 4 && (size_t)splits * m * w.rows <= ws_floats) {
+        if (g < 2 * cus && splits == 3 && (size_t)splits * m * w.rows <= ws_floats) {
             const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, true, 3 * cus);
             if (st != 1) return st;
         }
