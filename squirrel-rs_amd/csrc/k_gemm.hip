@@ -636,11 +636,10 @@ struct RowsEpi {
 // so every output element of a wavefront's gate tile has its up value at the
 // same register of the next tile; the 32 lanes of a half-wavefront then hold
 // one prompt row's FFN block, and SiLU(gate) * up and its Q8_0 block are
-// formed as silu_mul8_kernel forms them.  RW_QKV (128 x 64 tiles) applies
-// RoPE to the q and k columns (the pair partner of column n is column n ^ 1,
-// lane l ^ 1) and appends the K and V rows to the cache, as rope_kv_kernel
-// does.  The same operations on the same values as the separate kernels, so
-// the same bits.
+// formed as silu_mul8_kernel forms them.  RW_QKV applies RoPE to the q and
+// k columns (the pair partner of column n is column n ^ 1, lane l ^ 1) and
+// appends the K and V rows to the cache, as rope_kv_kernel does.  The same
+// operations on the same values as the separate kernels, so the same bits.
 typedef __attribute__((address_space(3))) int8_t lds_i8;
 
 template <int BM, int BN, int SKB>
@@ -712,7 +711,6 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kerne
     float* __restrict__ out, int ldo, int accumulate, int kbs, size_t split_stride, RowsEpi ep) {
     static_assert(BM == 128 && (BN == 64 || BN == 128), "tiles of 128 x 128 or 128 x 64");
     static_assert(EPI != RW_GATEUP || BN == 128, "the gate/up epilogue takes 128 x 128 tiles");
-    static_assert(EPI != RW_QKV || BN == 64, "the q|k|v epilogue takes 128 x 64 tiles");
     static_assert(ST >= 2 && ST <= 4, "two to four stages");
     static_assert(SKB == 2 || SKB == 4, "two or four blocks per stage");
     constexpr int SM = BM / 64, SN = BN / 64;
@@ -975,14 +973,15 @@ __global__ __launch_bounds__(256, (dma_occupancy<BM, BN>())) void gemm_dma_kerne
         return;
     }
     if constexpr (EPI == RW_QKV) {
-        const int QD = ep.q_dim, KVD = ep.kv_dim, n = n0 + wn + fr;
+        const int QD = ep.q_dim, KVD = ep.kv_dim;
 #pragma unroll
-        for (int i = 0; i < SM; i++)
+        for (int t = 0; t < NT; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float v = acc[i][r];
+                const float v = acc[t][r];
                 const float pv = __shfl_xor(v, 1, 64);  // column n ^ 1 of the same prompt row
-                const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
+                const int m = m0 + wm + 32 * (t / SN) + 8 * (r >> 2) + 4 * fh + (r & 3);
+                const int n = n0 + wn + 32 * (t % SN) + fr;
                 if (m >= m_rows || n >= w.rows) continue;
                 const int p = ep.pos0 + m;
                 if (n < QD + KVD) {
@@ -1047,6 +1046,38 @@ __global__ __launch_bounds__(256) void split_sum4_kernel(const float* __restrict
         v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
     }
     *o = v;
+}
+
+// The stacked q|k|v projection's K-split partials ([m][ncols] each, stride
+// apart) summed in split order as split_sum_kernel sums them, then RoPE on the
+// q and k columns and the KV-cache append as rope_kv_kernel applies them: one
+// workgroup per prompt row, the same operations on the same values.
+__global__ __launch_bounds__(256) void split_sum_rope_kernel(const float* __restrict__ ws, int splits, size_t stride,
+                                                             int ncols, RowsEpi ep) {
+    const int m = blockIdx.x, p = ep.pos0 + m;
+    const int QD = ep.q_dim, KVD = ep.kv_dim, half = ep.head_dim >> 1;
+    const float* row = ws + (size_t)m * ncols;
+    auto sum = [&](int e) {
+        float v = 0.0f;
+        for (int z = 0; z < splits; z++) v += row[z * stride + e];
+        return v;
+    };
+    for (int pi = threadIdx.x; pi < (QD + KVD) >> 1; pi += 256) {
+        const int e = 2 * pi;
+        const bool is_q = e < QD;
+        const int li = is_q ? e : e - QD;
+        const float2 cs = ep.rope[(size_t)p * half + ((li % ep.head_dim) >> 1)];
+        float o0, o1;
+        sq_rotate(sum(e), sum(e + 1), cs.x, cs.y, o0, o1);
+        if (is_q) {
+            ep.q_out[(size_t)m * QD + li] = o0;
+            ep.q_out[(size_t)m * QD + li + 1] = o1;
+        } else {
+            ep.kcache[(size_t)p * KVD + li] = o0;
+            ep.kcache[(size_t)p * KVD + li + 1] = o1;
+        }
+    }
+    for (int i = threadIdx.x; i < KVD; i += 256) ep.vcache[(size_t)p * KVD + i] = sum(QD + KVD + i);
 }
 
 // out (+)= the split partials in split order, on the vector kernel where the
@@ -1471,33 +1502,50 @@ int gemm_tile_override() {
 // Inputs the few-rows kernel takes unless a tiling is pinned: up to 32 rows.
 bool rows_kernel_fits(int m, int k) { return m <= 32 && (k / 32) % RW_NB == 0 && gemm_tile_override() == TILE_AUTO; }
 
+// The full-rate tiling an input of m >= 128 rows takes with no tiling
+// pinned (bn 0: neither; then the 64 x 64 kernel), shared by the plain path
+// and the fused epilogues so that both fold the same terms:
+//  - 128 x 128 tiles where they give every CU two workgroups;
+//  - for Q8_0 weights, where 128 x 128 tiles cover a third to a half of the
+//    device's three-per-CU slots, the same tiles with K split two or three
+//    ways (one round; the partials summed in split order): the o and FFN
+//    down projections of a 2048-token prompt (256 tiles) split three ways,
+//    its q|k|v projection (384 tiles) two -- about half the time of the
+//    unsplit 128 x 64 tiles for the down projection, whose 512 workgroups
+//    leave a third of the direct-to-LDS kernel's slots empty;
+//  - 128 x 64 tiles where those give every CU two workgroups.
+struct Tiling {
+    int bn, splits;
+};
+Tiling auto_tiling(const MatView& w, int wt, int m, bool have_ws, size_t ws_floats) {
+    if (m < 128) return {0, 1};
+    const int cus = device_cus(), gy = (m + 127) / 128, g = (w.rows + 127) / 128 * gy;
+    if (g >= 2 * cus) return {128, 1};
+    if (wt == WT_Q8_0 && w.k / 32 >= 64 && have_ws) {
+        const int splits = (3 * cus + g - 1) / g;
+        if (splits <= 3 && (size_t)splits * m * w.rows <= ws_floats) return {128, splits};
+    }
+    if ((w.rows + 63) / 64 * gy >= 2 * cus) return {64, 1};
+    return {0, 1};
+}
+
 template <int WT>
 int run_integer(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, float* out, int ldo,
                 bool acc, float* ws, size_t ws_floats) {
     const int tile = gemm_tile_override();
     if ((tile == TILE_ROWS && (w.k / 32) % RW_NB == 0) || rows_kernel_fits(m, w.k))
         return run_rows<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats);
-    if (tile == TILE_128 || (tile == TILE_AUTO && m >= 128)) {
-        const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128);
-        if (st != 1) return st;
-    }
-    // About one 128 x 128 tile per CU (the o and FFN down projections of a
-    // 2048-token prompt: 256 tiles, K = 2048 and 8192): split K three ways,
-    // so that the grid takes three workgroups per CU, one round, and sum the
-    // partials in split order (about half the time of the unsplit 128 x 64
-    // tiles for the down projection, whose 512 workgroups leave a third of
-    // the direct-to-LDS kernel's slots empty).
-    if (WT == WT_Q8_0 && tile == TILE_AUTO && m >= 128 && w.k / 32 >= 64 && ws != nullptr) {
-        const int cus = device_cus(), g = (w.rows + 127) / 128 * ((m + 127) / 128);
-        const int splits = (3 * cus + g - 1) / g;
-        if (g < 2 * cus && splits == 3 && (size_t)splits * m * w.rows <= ws_floats) {
-            const int st = run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, true, 3 * cus);
-            if (st != 1) return st;
-        }
-    }
-    if (tile == TILE_128X64 || (tile == TILE_AUTO && m >= 128)) {
-        const int st = run_mfma32<WT, 128, 64>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, tile == TILE_128X64);
-        if (st != 1) return st;
+    if (tile == TILE_128)
+        return run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, true);
+    if (tile == TILE_128X64)
+        return run_mfma32<WT, 128, 64>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, true);
+    if (tile == TILE_AUTO) {
+        const Tiling t = auto_tiling(w, WT, m, ws != nullptr, ws_floats);
+        const int g = (w.rows + 127) / 128 * ((m + 127) / 128);
+        if (t.bn == 128)
+            return run_mfma32<WT, 128, 128>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, true,
+                                            t.splits > 1 ? t.splits * g : 0);
+        if (t.bn == 64) return run_mfma32<WT, 128, 64>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats, true);
     }
     return run_mfma<WT>(s, w, aq, ad, m, out, ldo, acc, ws, ws_floats);
 }
@@ -1515,16 +1563,13 @@ bool prefill_fusion_enabled() {
 // tiling); -1 when it does not apply.
 template <int BN, int EPI>
 int run_dma_fused(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, int gx,
-                  const RowsEpi& ep) {
+                  const RowsEpi& ep, size_t ws_floats) {
     const int KB = w.k / 32, gy = (m + 127) / 128;
     if (w.wtype != WT_Q8_0 || KB % DMA_KB || !dma_offsets_fit(w, m) || !gemm_dma_enabled() ||
         gemm_tile_override() != TILE_AUTO)
         return -1;
-    if (gx * gy < 2 * device_cus()) return -1;
-    // the unfused path's choice for this grid: 128 x 128 tiles where those
-    // fill the device, else 128 x 64
-    const int g128 = (w.rows + 127) / 128 * gy;
-    if ((BN == 128) != (g128 >= 2 * device_cus())) return -1;
+    const Tiling t = auto_tiling(w, WT_Q8_0, m, ws_floats > 0, ws_floats);  // the unfused path's choice
+    if (t.bn != BN || t.splits != 1) return -1;
     count_launch(1, BN);
     hipLaunchKernelGGL((gemm_dma_kernel<128, BN, DMA_STAGES, DMA_KB, EPI>), dim3(gx, gy), dim3(256), 0, s, w, aq, ad, m,
                        nullptr, 0, 0, KB, (size_t)0, ep);
@@ -1538,7 +1583,7 @@ int run_dma_fused(hipStream_t s, const MatView& w, const int8_t* aq, const uint1
 // prompts on the direct-to-LDS kernel; -1 when it does not apply.
 template <int WT>
 int run_gateup_silu(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, int8_t* act_q,
-                    uint16_t* act_d) {
+                    uint16_t* act_d, size_t ws_floats) {
     const int ffn = w.rows / 2, KB = w.k / 32;
     if (w.rows % 2 || ffn % 32 || !prefill_fusion_enabled()) return -1;
     if (!rows_kernel_fits(m, w.k)) {
@@ -1546,7 +1591,7 @@ int run_gateup_silu(hipStream_t s, const MatView& w, const int8_t* aq, const uin
         RowsEpi ep{};
         ep.act_q = act_q;
         ep.act_d = act_d;
-        return run_dma_fused<128, RW_GATEUP>(s, w, aq, ad, m, ffn / 64, ep);
+        return run_dma_fused<128, RW_GATEUP>(s, w, aq, ad, m, ffn / 64, ep, ws_floats);
     }
     const int gx = ffn / 32, gy = (m + 31) / 32;
     if (gx * gy < device_cus()) return -1;  // the split-free two-tile form only
@@ -1561,12 +1606,38 @@ int run_gateup_silu(hipStream_t s, const MatView& w, const int8_t* aq, const uin
 // KV-cache append fused (one launch instead of two); -1 when it does not
 // apply.
 template <int WT>
-int run_qkv_rope(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, const RowsEpi& ep) {
+int run_qkv_rope(hipStream_t s, const MatView& w, const int8_t* aq, const uint16_t* ad, int m, const RowsEpi& ep,
+                 float* ws, size_t ws_floats) {
     const int KB = w.k / 32, gx = (w.rows + 31) / 32, gy = (m + 31) / 32;
     if (ep.head_dim % 2 || (ep.q_dim + ep.kv_dim) % 2 || w.rows != ep.q_dim + 2 * ep.kv_dim ||
         !prefill_fusion_enabled())
         return -1;
-    if (!rows_kernel_fits(m, w.k)) return run_dma_fused<64, RW_QKV>(s, w, aq, ad, m, (w.rows + 63) / 64, ep);
+    if (!rows_kernel_fits(m, w.k)) {
+        if (ws == nullptr) ws_floats = 0;
+        const Tiling t = auto_tiling(w, WT, m, ws_floats > 0, ws_floats);
+        if (t.bn == 64) return run_dma_fused<64, RW_QKV>(s, w, aq, ad, m, (w.rows + 63) / 64, ep, ws_floats);
+        if (t.bn == 128 && t.splits == 1)
+            return run_dma_fused<128, RW_QKV>(s, w, aq, ad, m, (w.rows + 127) / 128, ep, ws_floats);
+        // K split over 128 x 128 tiles: the partials, then their sum with
+        // RoPE and the KV append (the plain path's split sum, then RoPE)
+        if (WT != WT_Q8_0 || t.bn != 128 || KB % DMA_KB || !dma_offsets_fit(w, m) || !gemm_dma_enabled() ||
+            gemm_tile_override() != TILE_AUTO)
+            return -1;
+        // the plain path's K partition (run_mfma32)
+        const int chunks = (KB + M8_KB - 1) / M8_KB, kbs = (chunks + t.splits - 1) / t.splits * M8_KB;
+        if ((KB + kbs - 1) / kbs != t.splits || kbs % DMA_KB) return -1;
+        count_launch(t.splits, 128);
+        const size_t stride = (size_t)m * w.rows;
+        hipLaunchKernelGGL((gemm_dma_kernel<128, 128, DMA_STAGES, DMA_KB, RW_STORE>),
+                           dim3((w.rows + 127) / 128, (m + 127) / 128, t.splits), dim3(256), 0, s, w, aq, ad, m, ws,
+                           w.rows, 0, kbs, stride, RowsEpi{});
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("gemm launch: ") + hipGetErrorString(e));
+        hipLaunchKernelGGL(split_sum_rope_kernel, dim3(m), dim3(256), 0, s, ws, t.splits, stride, w.rows, ep);
+        e = hipGetLastError();
+        if (e != hipSuccess) return set_error(SQ_ERR_HIP, std::string("split sum launch: ") + hipGetErrorString(e));
+        return 0;
+    }
     // where run_rows would pair tiles or split K (other sums than the plain path's)
     if ((gx + 1) / 2 * gy >= device_cus() || (gx * gy < device_cus() && KB / (RW_NW * 2 * RW_NB) >= 2)) return -1;
     count_launch(1, 32);
@@ -1620,18 +1691,18 @@ void gemm_counters(bool reset, uint64_t* out) {
 }
 
 int launch_gateup_silu(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
-                       int8_t* act_q, uint16_t* act_d) {
+                       int8_t* act_q, uint16_t* act_d, size_t ws_floats) {
     if (w.k <= 0 || w.k % 32 != 0 || m <= 0) return -1;
     MatView v = w;
     v.wtype = wtype;
-    if (wtype == WT_Q8_0) return run_gateup_silu<WT_Q8_0>(s, v, aq, ad, m, act_q, act_d);
-    if (wtype == WT_Q4_0) return run_gateup_silu<WT_Q4_0>(s, v, aq, ad, m, act_q, act_d);
+    if (wtype == WT_Q8_0) return run_gateup_silu<WT_Q8_0>(s, v, aq, ad, m, act_q, act_d, ws_floats);
+    if (wtype == WT_Q4_0) return run_gateup_silu<WT_Q4_0>(s, v, aq, ad, m, act_q, act_d, ws_floats);
     return -1;
 }
 
 int launch_qkv_rope(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
                     int q_dim, int kv_dim, int head_dim, int pos0, const float2* rope, float* q_out, float* kcache,
-                    float* vcache) {
+                    float* vcache, float* ws, size_t ws_floats) {
     if (w.k <= 0 || w.k % 32 != 0 || m <= 0) return -1;
     MatView v = w;
     v.wtype = wtype;
@@ -1644,8 +1715,8 @@ int launch_qkv_rope(hipStream_t s, const MatView& w, int wtype, const int8_t* aq
     ep.kv_dim = kv_dim;
     ep.head_dim = head_dim;
     ep.pos0 = pos0;
-    if (wtype == WT_Q8_0) return run_qkv_rope<WT_Q8_0>(s, v, aq, ad, m, ep);
-    if (wtype == WT_Q4_0) return run_qkv_rope<WT_Q4_0>(s, v, aq, ad, m, ep);
+    if (wtype == WT_Q8_0) return run_qkv_rope<WT_Q8_0>(s, v, aq, ad, m, ep, ws, ws_floats);
+    if (wtype == WT_Q4_0) return run_qkv_rope<WT_Q4_0>(s, v, aq, ad, m, ep, ws, ws_floats);
     return -1;
 }
 

@@ -144,19 +144,22 @@ int launch_gemm(hipStream_t s, const MatView& w, int wtype, bool a8, const int8_
 // given as Q8_0, with silu(gate) * up written as Q8_0 blocks (act_q [m][ffn],
 // act_d [m][ffn / 32]) in the same launch: what launch_gemm followed by
 // launch_silu_mul_rows writes, bit for bit.  act_q/act_d must not overlap
-// aq/ad (every workgroup reads every row).  Returns -1 (nothing launched)
-// where the fused form does not apply (more than 32 rows, small grids).
+// aq/ad (every workgroup reads every row).  ws_floats: the workspace size
+// launch_gemm would be given (it picks the same tiling).  Returns -1
+// (nothing launched) where the fused form does not apply (small grids,
+// K-split tilings, pinned tilings).
 int launch_gateup_silu(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
-                       int8_t* act_q, uint16_t* act_d);
+                       int8_t* act_q, uint16_t* act_d, size_t ws_floats = 0);
 // The stacked q|k|v projection (w: q_dim + 2 kv_dim rows) of m prompt rows
 // at positions pos0.. given as Q8_0, with RoPE on q and k and the KV-cache
-// append in the same launch: what launch_gemm followed by
+// append in the same launch (or, on a K-split tiling, in the launch that sums
+// the partials in ws): what launch_gemm with the same workspace followed by
 // launch_rope_kv_rows writes, bit for bit (q_out [m][q_dim], the caches
 // [position][kv_dim]).  Returns -1 (nothing launched) where the fused form
-// does not apply (more than 32 rows).
+// does not apply.
 int launch_qkv_rope(hipStream_t s, const MatView& w, int wtype, const int8_t* aq, const uint16_t* ad, int m,
                     int q_dim, int kv_dim, int head_dim, int pos0, const float2* rope, float* q_out, float* kcache,
-                    float* vcache);
+                    float* vcache, float* ws = nullptr, size_t ws_floats = 0);
 
 // ---- persistent decode step (k_step.hip) -----------------------------------
 struct StepLayer {

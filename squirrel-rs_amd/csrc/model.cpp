@@ -642,10 +642,10 @@ int run_prefill(sq_ctx* c, size_t n) {
                                       a8 ? c->p_aq : nullptr, c->p_ad)) ||
             (st = tap(l, 0, D)))
             return st;
-        // short prompts: the q|k|v projection, RoPE and the KV append in one launch
+        // the q|k|v projection with RoPE and the KV append in its epilogue
         if ((st = phase(0))) return st;
         const int fused_qkv = a8 ? launch_qkv_rope(s, view(L.qkv), m->wtype, c->p_aq, c->p_ad, N, QD, KVD, hd, pos0,
-                                                   c->rope, c->p_q, kc, vc)
+                                                   c->rope, c->p_q, kc, vc, c->p_split, kPrefillSplitFloats)
                                  : -1;
         if (fused_qkv > 0) return fused_qkv;
         if (fused_qkv != 0) {
@@ -686,7 +686,8 @@ int run_prefill(sq_ctx* c, size_t n) {
         if (a8) {
             int8_t* aq2 = (int8_t*)c->p_act;
             uint16_t* ad2 = (uint16_t*)(aq2 + (size_t)N * F);
-            fused = launch_gateup_silu(s, view(L.gateup), m->wtype, c->p_aq, c->p_ad, N, aq2, ad2);
+            fused = launch_gateup_silu(s, view(L.gateup), m->wtype, c->p_aq, c->p_ad, N, aq2, ad2,
+                                       kPrefillSplitFloats);
             if (fused > 0) return fused;
             if (fused == 0) {
                 fq = aq2;

@@ -241,7 +241,17 @@ int main(int argc, char** argv) {
     for (int step = 0; step <= n_decode; step++) {
         const uint32_t* p = step == 0 ? ids.data() : ids.data() + n_prompt + step - 1;
         const size_t n = step == 0 ? (size_t)n_prompt : 1;
+        if (step == 0) sq_gemm_counters(1, nullptr);
         if ((st = sq_forward(m, c, p, n))) die("sq_forward", st);
+        if (step == 0) {
+            // the prefill's matmul launches: all, K-split, 128 x 128 tiles,
+            // most splits, 128 x 64 tiles, few-rows kernel
+            uint64_t gc[6];
+            sq_gemm_counters(0, gc);
+            printf("gemm launches %llu split %llu tile128 %llu max_splits %llu tile128x64 %llu rows %llu\n",
+                   (unsigned long long)gc[0], (unsigned long long)gc[1], (unsigned long long)gc[2],
+                   (unsigned long long)gc[3], (unsigned long long)gc[4], (unsigned long long)gc[5]);
+        }
         if ((st = sq_logits(c, got.data(), got.size()))) die("sq_logits", st);
         uint32_t tok = 0;
         if ((st = sq_argmax(c, &tok))) die("sq_argmax", st);

@@ -190,6 +190,48 @@ def test_long_prefill_fused_epilogues_in_bounds(emu, models, unfused):
     assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
 
 
+@pytest.fixture(scope="module")
+def wide_model(emu, tmp_path_factory):
+    """One layer at Llama-3.2-1B's width (dim 2048, 32 heads, 8 KV heads; a
+    256-wide FFN keeps the emulated run short): the q|k|v projection has
+    3072 rows and K = 2048."""
+    path = str(tmp_path_factory.mktemp("emu_wide") / "w2k_Q8_0.gguf")
+    subprocess.run([emu, "--write", path, str(Q8_0), "7", "1", "2048", "256", "32", "8", "512"], check=True, env=ENV)
+    return path
+
+
+def gemm_counts(out):
+    m = re.search(r"^gemm launches (\d+) split (\d+) tile128 (\d+) max_splits (\d+) tile128x64 (\d+) rows (\d+)",
+                  out, re.M)
+    return dict(zip(("launches", "split", "tile128", "max_splits", "tile128x64", "rows"), map(int, m.groups())))
+
+
+@pytest.mark.parametrize("cus,want", [
+    # 48 tiles of 128 x 128 fill 8 CUs twice: the q|k|v projection with
+    # RoPE and the KV append in the 128 x 128 kernel's epilogue
+    (8, {"launches": 4, "split": 1, "tile128": 4, "tile128x64": 0}),
+    # 48 tiles on 32 CUs: K split two ways, RoPE and the KV append in the
+    # kernel that sums the partials (the o projection splits three ways)
+    (32, {"launches": 4, "split": 3, "tile128": 2, "tile128x64": 1}),
+])
+def test_wide_prefill_qkv_epilogues(emu, wide_model, cus, want):
+    """A 140-row prefill of the full-width layer on an emulated 8- and
+    32-CU device: the fused q|k|v forms (the 128 x 128 epilogue; the K-split
+    sum with RoPE) stay in bounds, match the oracle, and give the same
+    logits, hidden state and quantization-site flips as the separate
+    launches (SQUIRREL_PREFILL_UNFUSED=1)."""
+    lines = {}
+    for unfused in ("0", "1"):
+        steps, out = run(emu, [wide_model, W8A8, MULTI_KERNEL, 140, 0, 1, 160],
+                         env={"SQEMU_CUS": str(cus), "SQUIRREL_PREFILL_UNFUSED": unfused})
+        assert len(steps) == 1 and steps[0][1] <= 1e-6 and steps[0][3] == steps[0][4], out
+        assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
+        n = gemm_counts(out)
+        assert {k: n[k] for k in want} == want, n
+        lines[unfused] = re.findall(r"^(?:step|lock step) .*$", out, re.M)
+    assert lines["0"] == lines["1"], lines
+
+
 @pytest.mark.parametrize("step,layer,site,element,kind", [
     (0, 0, 0, 100, 0),   # prefill, attention-norm output, one element
     (0, 1, 3, 700, 1),   # prefill, FFN activation, one block scale

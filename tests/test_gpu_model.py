@@ -684,27 +684,30 @@ def test_full_width_long_context_decode(model_dir):
 
 
 @FULL
-def test_long_prompt_fused_epilogues_bit_exact(model_dir, monkeypatch):
-    """1B widths (2 layers), Q8_0, a 2048-token prompt: the gate/up projection
-    (128 x 128 tiles) forms SiLU * up and its Q8_0 blocks in its epilogue, the
-    q|k|v projection (128 x 64 tiles) applies RoPE and appends to the KV
-    cache.  With the fusions off (SQUIRREL_PREFILL_UNFUSED=1: the same matmul
-    kernels, then the separate SiLU and RoPE kernels) the prefill and the
-    decode steps after it give the same logits bit for bit; so do the
-    register-staged matmul kernels (SQUIRREL_GEMM_DMA=0, which also turns the
-    fusions off)."""
+@pytest.mark.parametrize("n_prompt,splits", [(2048, 6), (4096, 0)])
+def test_long_prompt_fused_epilogues_bit_exact(model_dir, monkeypatch, n_prompt, splits):
+    """1B widths (2 layers), Q8_0, 2048- and 4096-token prompts, every matmul
+    on 128 x 128 tiles: the gate/up projection forms SiLU * up and its Q8_0
+    blocks in its epilogue; the q|k|v projection applies RoPE and appends to
+    the KV cache in its epilogue (4096 tokens: 768 tiles) or, with K split
+    two ways (2048 tokens: 384 tiles), in the kernel that sums the partials
+    (the o and down projections split three ways there).  With the fusions
+    off (SQUIRREL_PREFILL_UNFUSED=1: the same matmul kernels, then the
+    separate SiLU and RoPE kernels) the prefill and the decode steps after it
+    give the same logits bit for bit; so do the register-staged matmul
+    kernels (SQUIRREL_GEMM_DMA=0, which also turns the fusions off)."""
     from sqhip import ops
     path = full_model(model_dir, "Q8_0", n_layers=2)
-    seq = full_seq(2048, 2, 6)
+    seq = full_seq(n_prompt, 2, 6)
     ops.gemm_counters(reset=True)
-    fused, toks_f, _ = run_gpu(path, seq, max_pos=2056, taps=False)
+    fused, toks_f, _ = run_gpu(path, seq, max_pos=n_prompt + 8, taps=False)
     n = ops.gemm_counters(reset=True)
-    assert n["tile128_launches"] == 6 and n["tile128x64_launches"] == 2 and n["split_launches"] == 4, n
+    assert n["tile128_launches"] == 8 and n["tile128x64_launches"] == 0 and n["split_launches"] == splits, n
     monkeypatch.setenv("SQUIRREL_PREFILL_UNFUSED", "1")
-    plain, toks_p, _ = run_gpu(path, seq, max_pos=2056, taps=False)
+    plain, toks_p, _ = run_gpu(path, seq, max_pos=n_prompt + 8, taps=False)
     monkeypatch.delenv("SQUIRREL_PREFILL_UNFUSED")
     monkeypatch.setenv("SQUIRREL_GEMM_DMA", "0")
-    staged, toks_s, _ = run_gpu(path, seq, max_pos=2056, taps=False)
+    staged, toks_s, _ = run_gpu(path, seq, max_pos=n_prompt + 8, taps=False)
     assert toks_f == toks_p == toks_s
     for step, (a, b, c) in enumerate(zip(fused, plain, staged)):
         assert np.array_equal(a, b), f"step {step}: the fused and the separate forms differ"
@@ -715,14 +718,14 @@ def test_long_prompt_fused_epilogues_bit_exact(model_dir, monkeypatch):
 def test_full_width_prefill_2048(model_dir):
     """1B widths (2 layers): a 2048-token batched prefill -- every matmul on
     the full-rate matrix-core kernel: per layer the gate/up projection on
-    128 x 128 tiles (2048 tiles), the QKV projection on 128 x 64 tiles (768),
-    the o and down projections on 128 x 128 tiles (256) with K split three ways
-    (768 workgroups), causal attention over 2048 x 2048 per head -- then the
-    workload's 15 decode steps."""
+    128 x 128 tiles (2048 tiles), the QKV projection on 128 x 128 tiles (384)
+    with K split two ways, the o and down projections on 128 x 128 tiles (256)
+    with K split three ways (768 workgroups), causal attention over
+    2048 x 2048 per head -- then the workload's 15 decode steps."""
     from sqhip import ops
     ops.gemm_counters(reset=True)
     check_full(full_model(model_dir, "Q8_0", n_layers=2), full_seq(2048, 15, 3), "1B-wide prefill 2048+15",
                max_pos=2064)
     n = ops.gemm_counters(reset=True)
-    assert n == {"launches": 8, "split_launches": 4, "tile128_launches": 6, "max_splits": 3,
-                 "tile128x64_launches": 2, "rows_launches": 0}, n
+    assert n == {"launches": 8, "split_launches": 6, "tile128_launches": 8, "max_splits": 3,
+                 "tile128x64_launches": 0, "rows_launches": 0}, n
