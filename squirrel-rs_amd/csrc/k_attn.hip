@@ -8,6 +8,9 @@
 //
 // Cache layout (KvCache, src/models/common/kv_cache.rs:1-16): per layer
 // [position][n_kv_heads * head_dim] f32, row-major.
+#include <cstdlib>
+#include <cstring>
+
 #include "launch.h"
 
 namespace sq {
@@ -390,6 +393,306 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
     }
 }
 
+// The same attention with its products on the f16 matrix instructions
+// (v_mfma_f32_16x16x32_f16, 16 times the fp32 rate): every f32 operand x is
+// split into hi = f16(x) (round to nearest even) and lo = f16((x - hi) 2^11),
+// and a product a b is formed as hi_a hi_b + 2^-11 (hi_a lo_b + lo_a hi_b),
+// accumulated in f32.  hi carries x's leading 11 bits and lo the next 11,
+// so the dropped lo_a lo_b term and lo's rounding leave a relative error of
+// about 2^-22 per product, against 2^-24 for one f32 rounding: the attention
+// output stays within f32 rounding noise of the fp32 kernel.  Scaling lo by
+// 2^11 keeps it a normal f16 whenever hi is one; q, k and v are scaled by
+// 2^-8 before the split (power-of-two scalings, undone exactly in the
+// scores and the output), so hi overflows only for |x| >= 2^23.
+//
+// Layout: lane l supplies A[l % 16][8 (l / 16) .. +7] and
+// B[8 (l / 16) .. +7][l % 16]; result r of lane l is D[4 (l / 16) + r][l % 16].
+// Scores are formed transposed as in attn_prefill_kernel (S^T = K Q^T, key
+// rows as the row operand): lane l holds keys 4 (l / 16) + 0..3 of each
+// 16-key subtile for query l % 16.  For O^T = V^T P^T over a 32-key half u of
+// the tile, lane l's eight contraction slots 8 (l / 16) + j take keys
+// 32 u + 4 (l / 16) + j (j < 4) and 32 u + 16 + 4 (l / 16) + j - 4 (j >= 4),
+// which are its own probabilities of subtiles 2 u and 2 u + 1; V^T is staged
+// in LDS with its keys in that slot order, so the probabilities never leave
+// the registers here either.
+typedef _Float16 as_v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 as_v2h __attribute__((ext_vector_type(2)));
+typedef float as_v2f __attribute__((ext_vector_type(2)));
+constexpr int SLD = HD + 8;                 // padded LDS row (halves): 144 bytes
+constexpr float kLoUp = 2048.0f;            // 2^11
+constexpr float kLoDown = 1.0f / 2048.0f;   // 2^-11
+constexpr float kPre = 1.0f / 256.0f;       // 2^-8 on q, k and v
+
+// hi and lo of two values, each pair packed into 32 bits
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    const as_v2f v = {a * kPre, b * kPre};
+    const as_v2h h = __builtin_convertvector(v, as_v2h);
+    const as_v2f back = __builtin_convertvector(h, as_v2f);
+    const as_v2h l = __builtin_convertvector((v - back) * kLoUp, as_v2h);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+// the same without the 2^-8 (probabilities)
+__device__ __forceinline__ void split2p(float a, float b, uint32_t& hi, uint32_t& lo) {
+    const as_v2f v = {a, b};
+    const as_v2h h = __builtin_convertvector(v, as_v2h);
+    const as_v2f back = __builtin_convertvector(h, as_v2f);
+    const as_v2h l = __builtin_convertvector((v - back) * kLoUp, as_v2h);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+__device__ __forceinline__ as_v8h pack8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(as_v8h, u4{a, b, c, d});
+}
+// slot of key kk (0..63) in the staged V^T rows
+__device__ __forceinline__ int v_slot(int kk) {
+    const int u = kk >> 5, k = kk & 31;
+    return 32 * u + 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3);
+}
+
+__global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float* __restrict__ q,
+                                                                  const float* __restrict__ kc,
+                                                                  const float* __restrict__ vc, int pos0,
+                                                                  int m_rows, int n_heads, int n_kv_heads,
+                                                                  float* __restrict__ out,
+                                                                  int8_t* __restrict__ act_q,
+                                                                  uint16_t* __restrict__ act_d) {
+    __shared__ __attribute__((aligned(16))) _Float16 s_kh[PT][SLD];  // [key][dim]
+    __shared__ __attribute__((aligned(16))) _Float16 s_kl[PT][SLD];
+    __shared__ __attribute__((aligned(16))) _Float16 s_vh[HD][SLD];  // [dim][key slot]
+    __shared__ __attribute__((aligned(16))) _Float16 s_vl[HD][SLD];
+
+    const int h = blockIdx.x;
+    // query tiles in the order of attn_prefill_kernel (equal causal work per CU)
+    int ty = blockIdx.y;
+    if ((gridDim.y & 3) == 0) {
+        const int B = gridDim.y >> 2, k = ty / B, a = ty % B;
+        ty = k == 0 ? a : k == 1 ? 4 * B - 1 - a : k == 2 ? B + a : 3 * B - 1 - a;
+    }
+    const int t0 = ty * PT;
+    const int g = h / (n_heads / n_kv_heads);
+    const int q_dim = n_heads * HD;
+    const int kv_dim = n_kv_heads * HD;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lk = lane >> 4;
+    // base-2 scores of the 2^-8-scaled operands: s' = (q . k) 2^16 scale log2(e)
+    const float scale2 = (1.0f / sqrtf((float)HD)) * 1.44269504088896341f * 65536.0f;
+
+    // this lane's query (t0 + 16 wave + li), dims 32 c + 8 lk .. +7 as the
+    // column operand of chunk c
+    const int tq = t0 + 16 * wave + li;
+    as_v8h qh[2], ql[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (tq < m_rows) {
+            const float* src = q + (size_t)tq * q_dim + h * HD + 32 * c + 8 * lk;
+            const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+            x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        }
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) split2(x[2 * j], x[2 * j + 1], hi[j], lo[j]);
+        qh[c] = pack8(hi[0], hi[1], hi[2], hi[3]);
+        ql[c] = pack8(lo[0], lo[1], lo[2], lo[3]);
+    }
+    // online softmax state as in attn_prefill_kernel; the output accumulates
+    // as oh + 2^-11 ox, oh[dt][r] / ox[dt][r] at O^T[16 dt + 4 lk + r][tq]
+    float mrow = -INFINITY, lpart = 0.0f;
+    am_v4f oh[4], ox[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) oh[dt] = ox[dt] = am_v4f{0.f, 0.f, 0.f, 0.f};
+
+    const int last_q = min(t0 + PT, m_rows) - 1;
+    const int n_keys = pos0 + last_q + 1;
+    const int limit = pos0 + tq;
+    const int unmasked_end = pos0 + t0 + 1;
+
+    // Staging.  K: this thread's four 16-byte units (row e / 16, dims
+    // 4 (e % 16) ..) for e = tid + 256 i.  V: two key pairs (keys 2 p, 2 p + 1
+    // with p = e % 32, dims 4 (e / 32) ..) for e = tid + 256 i, i < 2, so that
+    // each dim's two halves go to adjacent slots (keys 2 p and 2 p + 1 differ
+    // in their slot's last bit) as one 32-bit write.  Rows past the last key
+    // read the last key (finite values; their probabilities are zero).
+    am_v4f kreg[4], vreg[4];
+    auto load_k = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
+            kreg[i] = *(const am_v4f*)(kc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
+        }
+    };
+    auto load_v = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int e = tid + 256 * i, p = e & 31, c4 = e >> 5;
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+                vreg[2 * i + s] =
+                    *(const am_v4f*)(vc + (size_t)min(kb + 2 * p + s, n_keys - 1) * kv_dim + g * HD + 4 * c4);
+        }
+    };
+    auto store_k = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
+            uint32_t h0, l0, h1, l1;
+            split2(kreg[i][0], kreg[i][1], h0, l0);
+            split2(kreg[i][2], kreg[i][3], h1, l1);
+            *(uint2*)&s_kh[r][4 * c4] = make_uint2(h0, h1);
+            *(uint2*)&s_kl[r][4 * c4] = make_uint2(l0, l1);
+        }
+    };
+    auto store_v = [&]() {  // transposed, keys in slot order
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int e = tid + 256 * i, p = e & 31, c4 = e >> 5;
+            const int slot = v_slot(2 * p);
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                uint32_t hv, lv;
+                split2(vreg[2 * i][d], vreg[2 * i + 1][d], hv, lv);
+                *(uint32_t*)&s_vh[4 * c4 + d][slot] = hv;
+                *(uint32_t*)&s_vl[4 * c4 + d][slot] = lv;
+            }
+        }
+    };
+    load_k(0);
+    load_v(0);
+    store_k();
+    __syncthreads();
+    for (int k0 = 0; k0 < n_keys; k0 += PT) {
+        const bool more = k0 + PT < n_keys;
+        // S^T for 4 subtiles of 16 keys: sc[t][r] = score of key k0 + 16 t + 4 lk + r
+        am_v4f sc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            asm volatile("" ::: "memory");
+            am_v4f hh = {0.f, 0.f, 0.f, 0.f}, xx = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const as_v8h kh = *(const as_v8h*)&s_kh[16 * t + li][32 * c + 8 * lk];
+                const as_v8h kl = *(const as_v8h*)&s_kl[16 * t + li][32 * c + 8 * lk];
+                hh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], hh, 0, 0, 0);
+                xx = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], xx, 0, 0, 0);
+                xx = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[c], xx, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) sc[t][r] = fmaf(xx[r], kLoDown, hh[r]);
+        }
+        store_v();
+        if (more) load_k(k0 + PT);
+        float tmax = -INFINITY;
+        if (k0 + PT > unmasked_end) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int kk = k0 + 16 * t + 4 * lk + r;
+                    sc[t][r] = kk <= limit ? sc[t][r] * scale2 : -INFINITY;
+                    tmax = fmaxf(tmax, sc[t][r]);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    sc[t][r] *= scale2;
+                    tmax = fmaxf(tmax, sc[t][r]);
+                }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mn = fmaxf(mrow, tmax);
+        const float alpha = __builtin_amdgcn_exp2f(mrow - mn);
+        float rsum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = __builtin_amdgcn_exp2f(sc[t][r] - mn);
+                sc[t][r] = p;
+                rsum += p;
+            }
+        lpart = lpart * alpha + rsum;
+        mrow = mn;
+        // P^T operands of the two 32-key halves
+        as_v8h ph[2], pl[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            uint32_t hi[4], lo[4];
+            split2p(sc[2 * u][0], sc[2 * u][1], hi[0], lo[0]);
+            split2p(sc[2 * u][2], sc[2 * u][3], hi[1], lo[1]);
+            split2p(sc[2 * u + 1][0], sc[2 * u + 1][1], hi[2], lo[2]);
+            split2p(sc[2 * u + 1][2], sc[2 * u + 1][3], hi[3], lo[3]);
+            ph[u] = pack8(hi[0], hi[1], hi[2], hi[3]);
+            pl[u] = pack8(lo[0], lo[1], lo[2], lo[3]);
+        }
+        __syncthreads();  // V staged; every wavefront is done with s_kh / s_kl
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            asm volatile("" ::: "memory");
+            am_v4f ah = oh[dt] * alpha, ax = ox[dt] * alpha;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const as_v8h vh = *(const as_v8h*)&s_vh[16 * dt + li][32 * u + 8 * lk];
+                const as_v8h vl = *(const as_v8h*)&s_vl[16 * dt + li][32 * u + 8 * lk];
+                ah = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[u], ah, 0, 0, 0);
+                ax = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[u], ax, 0, 0, 0);
+                ax = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[u], ax, 0, 0, 0);
+            }
+            oh[dt] = ah;
+            ox[dt] = ax;
+        }
+        if (more) {
+            store_k();
+            load_v(k0 + PT);
+        }
+        __syncthreads();  // the next K staged; every wavefront is done with s_vh / s_vl
+    }
+    float lrow = lpart + __shfl_xor(lpart, 16, 64);
+    lrow += __shfl_xor(lrow, 32, 64);
+    const float inv = 256.0f / lrow;  // undoes v's 2^-8
+    float y[4][4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) y[dt][c] = fmaf(ox[dt][c], kLoDown, oh[dt][c]) * inv;
+    if (out != nullptr && tq < m_rows) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            float* dst = out + (size_t)tq * q_dim + h * HD + 16 * dt + 4 * lk;
+            *(float4*)dst = make_float4(y[dt][0], y[dt][1], y[dt][2], y[dt][3]);
+        }
+    }
+    if (act_q != nullptr) {
+        // the row's Q8_0 blocks, as attn_prefill_kernel forms them
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int dt = 2 * b; dt < 2 * b + 2; dt++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) mx = fmaxf(mx, fabsf(y[dt][c]));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float scale = sq_q8_scale(fmaxf(mx, 0.0f)), qinv = sq_q8_inv(scale);
+            if (tq < m_rows) {
+#pragma unroll
+                for (int dt = 2 * b; dt < 2 * b + 2; dt++) {
+                    unsigned wq = 0;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) wq |= (unsigned)(uint8_t)sq_q8_quant(y[dt][c], qinv) << (8 * c);
+                    *(unsigned*)(act_q + (size_t)tq * q_dim + h * HD + 16 * dt + 4 * lk) = wq;
+                }
+                if (lk == 0) act_d[(size_t)tq * (q_dim / 32) + h * (HD / 32) + b] = sq_f32_to_f16(scale);
+            }
+        }
+    }
+}
+
 // Any head_dim (operator-level entry): one wavefront per (query, head) row,
 // scores in dynamic LDS.  Follows sdpa_f32 step by step: scores, softmax
 // (max, exp, 1/sum), then out = sum_s p_s * v_s in position order.
@@ -431,6 +734,14 @@ __global__ __launch_bounds__(64) void sdpa_generic_kernel(const float* q, const 
     }
 }
 
+// SQUIRREL_ATTN_F32=1 runs the prefill attention on the fp32 matrix
+// instructions (attn_prefill_kernel) instead of the split f16 ones (a test
+// and measurement aid).
+bool attn_f32_pinned() {
+    const char* e = getenv("SQUIRREL_ATTN_F32");
+    return e && !strcmp(e, "1");
+}
+
 }  // namespace
 
 int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const float* vcache, const int* pos,
@@ -458,8 +769,12 @@ int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, cons
                         uint16_t* act_d) {
     if (head_dim != HD) return set_error(SQ_ERR_UNSUPPORTED, "attention kernels are built for head_dim 64");
     dim3 grid(n_heads, (m + PT - 1) / PT);
-    hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos0, m, n_heads,
-                       n_kv_heads, out, act_q, act_d);
+    if (attn_f32_pinned())
+        hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos0, m, n_heads,
+                           n_kv_heads, out, act_q, act_d);
+    else
+        hipLaunchKernelGGL(attn_prefill_split_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos0, m, n_heads,
+                           n_kv_heads, out, act_q, act_d);
     return check_launch("attn_prefill");
 }
 

@@ -264,6 +264,31 @@ inline sqemu_v4f mfma_f32_16x16x16f16(sqemu_v4h a, sqemu_v4h b, sqemu_v4f c) {
     }
     return d;
 }
+// v_mfma_f32_16x16x32_f16: lane l supplies A[l%16][8(l/16) .. +7] and
+// B[8(l/16) .. +7][l%16] as eight halves; the sum is formed in double and
+// rounded once (every product of two halves is exact in f32).
+typedef _Float16 sqemu_v8h __attribute__((ext_vector_type(8)));
+inline sqemu_v4f mfma_f32_16x16x32f16(sqemu_v8h a, sqemu_v8h b, sqemu_v4f c) {
+    uint64_t mine[4];
+    memcpy(&mine[0], &a, 16);
+    memcpy(&mine[2], &b, 16);
+    const uint64_t* all = wave_exchange_n(mine, 4, 0x4005);
+    const int lane = g_lane;
+    const int col = lane & 15;
+    sqemu_v4f d = c;
+    for (int r = 0; r < 4; r++) {
+        const int row = 4 * (lane >> 4) + r;
+        double s = d[r];
+        for (int k = 0; k < 32; k++) {
+            _Float16 av, bv;
+            memcpy(&av, (const char*)&all[4 * (row + 16 * (k >> 3))] + 2 * (k & 7), 2);
+            memcpy(&bv, (const char*)&all[4 * (col + 16 * (k >> 3)) + 2] + 2 * (k & 7), 2);
+            s += (double)av * (double)bv;
+        }
+        d[r] = (float)s;
+    }
+    return d;
+}
 // 32 x 32 results: element r of lane l is D[8(r/4) + 4(l/32) + r%4][l%32].
 typedef int sqemu_v16i __attribute__((ext_vector_type(16)));
 typedef float sqemu_v16f __attribute__((ext_vector_type(16)));
@@ -341,6 +366,7 @@ inline sqemu_v16f mfma_f32_32x32x8f16(sqemu_v4h a, sqemu_v4h b, sqemu_v16f c) {
 #define __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, x, y, z) ::sqemu::mfma_i32_16x16x32_i8((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, x, y, z) ::sqemu::mfma_f32_16x16x4f32((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, x, y, z) ::sqemu::mfma_f32_16x16x16f16((a), (b), (c))
+#define __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, x, y, z) ::sqemu::mfma_f32_16x16x32f16((a), (b), (c))
 #define __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, x, y, z) ::sqemu::mfma_i32_32x32x32_i8((a), (b), (c))
 #define __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, x, y, z) ::sqemu::mfma_f32_32x32x8f16((a), (b), (c))
 #define __shfl_xor(v, m, w) ::sqemu::shfl_xor((v), (m), (w))

@@ -442,6 +442,50 @@ def test_sdpa_model_kernels_match_oracle(seq_q, seq_k, nh, nkv):
     assert np.allclose(got, want, rtol=1e-5, atol=2e-6), float(np.abs(got - want).max())
 
 
+@pytest.mark.parametrize("scale", [1e-3, 1.0, 6.0])
+def test_prefill_attention_split_f16_within_f32_noise(scale, monkeypatch):
+    """The prefill attention's split-f16 products (hi + 2^-11 lo halves of
+    every f32 operand) against the oracle, beside the fp32 matrix kernel
+    (SQUIRREL_ATTN_F32=1) on the same inputs: over operand magnitudes from
+    1e-3 (f16 subnormal hi halves) to 6 (sharp softmax rows), the split
+    kernel's largest error stays within a small multiple of the fp32
+    kernel's, i.e. within f32 rounding noise."""
+    seq_q, seq_k, nh, nkv, hd = 130, 300, 8, 2, 64
+    r = rng(int(scale * 1000) + 7)
+    q = (r.standard_normal(seq_q * nh * hd) * scale).astype(np.float32)
+    k = (r.standard_normal(seq_k * nkv * hd) * scale).astype(np.float32)
+    v = (r.standard_normal(seq_k * nkv * hd) * scale).astype(np.float32)
+    st, want = O.sdpa(q, k, v, seq_q, seq_k, nh, nkv, hd)
+    assert st == 0
+    got = sdpa_dev(q, k, v, seq_q, seq_k, nh, nkv, hd)
+    monkeypatch.setenv("SQUIRREL_ATTN_F32", "1")
+    ref = sdpa_dev(q, k, v, seq_q, seq_k, nh, nkv, hd)
+    e_split = float(np.abs(got - want).max()) / scale
+    e_f32 = float(np.abs(ref - want).max()) / scale
+    print(f"scale {scale}: max error / scale: split {e_split:.3e}, fp32 {e_f32:.3e}")
+    assert np.isfinite(got).all()
+    assert e_split <= max(4 * e_f32, 2e-6), (e_split, e_f32)
+
+
+def test_prefill_attention_large_operands():
+    """Operands up to 3e4 (beyond f16's range before the kernel's 2^-8
+    scaling) stay finite and match the oracle: the softmax rows are then
+    nearly one-hot, so the output is a v row to f32 rounding."""
+    seq_q, seq_k, nh, nkv, hd = 70, 70, 4, 4, 64
+    r = rng(99)
+    q = r.standard_normal(seq_q * nh * hd).astype(np.float32)
+    k = r.standard_normal(seq_k * nkv * hd).astype(np.float32)
+    v = r.standard_normal(seq_k * nkv * hd).astype(np.float32)
+    q[::97] = 3e4
+    k[::89] = -2e4
+    v[::83] = 3e4
+    st, want = O.sdpa(q, k, v, seq_q, seq_k, nh, nkv, hd)
+    assert st == 0
+    got = sdpa_dev(q, k, v, seq_q, seq_k, nh, nkv, hd)
+    assert np.isfinite(got).all()
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5 * 3e4), float(np.abs(got - want).max())
+
+
 def test_sdpa_generic_head_dims():
     for hd, nh, nkv, sq_, sk in [(4, 2, 1, 3, 5), (32, 4, 2, 1, 9), (128, 2, 2, 4, 4)]:
         r = rng(hd)
