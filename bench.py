@@ -18,8 +18,9 @@ fixed seed (synthetic data; no checkpoint is available).
 One JSON line is printed.  `roofline` prices the decode step (one persistent
 kernel launch per token) against MI355X's 8 TB/s HBM peak using its
 algorithmic bytes and its mean duration measured here with HIP events; the
-prefill block prices its integer matmuls against the 5.0 POP/s int8 and its
-attention against the 157.3 TFLOP/s fp32 matrix-core peaks.
+prefill block prices its integer matmuls against the 5.0 POP/s int8 peak and
+its attention (f32 operands split into f16 halves, three f16 products per
+f32 product) against the 2.5 PFLOP/s f16 matrix-core peak.
 `cpu_baseline` is the oracle (the C restatement of the reference's x86 scalar
 path) timed on this host, on the reference's thread count (all available
 logical cores), over a bounded sample of the headline workload.
@@ -43,6 +44,11 @@ METRIC = "decode tok/s batch-1 (1B Q8_0/Q4_0) + % HBM roofline; prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0     # dense int8 matrix-core peak
 FP32_MFMA_PEAK_TFLOPS = 157.3
+F16_MFMA_PEAK_TFLOPS = 2500.0  # dense f16 matrix-core peak
+# f16 matrix products per f32 product in the prefill attention (hi*hi,
+# hi*lo, lo*hi of the split operands); SQUIRREL_ATTN_F32=1 runs it on the
+# fp32 matrix instructions instead
+ATTN_F16_PRODUCTS = 3
 # Matrix elements per layer of the 1B shape: QKV 2048x3072, o 2048x2048,
 # gate/up 2048x16384, down 8192x2048.
 MATMUL_ELEMS_PER_LAYER = 60817408
@@ -238,8 +244,13 @@ def run_workload(name: str, cfg: dict, K: int, W: int, seed: int, kernel_iters: 
             "matmul_valu_rescale_ceiling_tops": round(valu_ceiling, 1),
             "matmul_frac_of_rescale_ceiling": round(mm_tops / valu_ceiling, 4),
             "attention_tflops": round(at_tflops, 1),
-            "attention_frac_of_fp32_mfma_peak": round(at_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
             "matmul_ops": mm_ops, "attention_flops": attn_flops}
+        if os.environ.get("SQUIRREL_ATTN_F32") == "1":
+            block["prefill_mfma"]["attention_frac_of_fp32_mfma_peak"] = round(at_tflops / FP32_MFMA_PEAK_TFLOPS, 4)
+        else:
+            f16_tflops = ATTN_F16_PRODUCTS * at_tflops
+            block["prefill_mfma"]["attention_f16_mfma_tflops"] = round(f16_tflops, 1)
+            block["prefill_mfma"]["attention_frac_of_f16_mfma_peak"] = round(f16_tflops / F16_MFMA_PEAK_TFLOPS, 4)
         block["prefill_roofline"] = {"bound": "mfma", "achieved": round(mm_tops, 1), "peak": INT8_PEAK_TOPS,
                                      "unit": "TOP/s", "frac": round(mm_tops / INT8_PEAK_TOPS, 4),
                                      "kernel": "gemm_mfma32_kernel (v_mfma_i32_32x32x32_i8 on 128x128 or "

@@ -461,8 +461,10 @@ int sq_sdpa(const float* d_q, const float* d_k, const float* d_v, float* d_out, 
                                          nullptr, nullptr));
     }
     if (model_kernels) {
+        Tmp kvs;
+        if ((st = kvs.alloc(attn_split_words((int)seq_k, (int)n_kv_heads) * 4))) return st;
         return finish(launch_attn_prefill(nullptr, d_q, d_k, d_v, (int)(seq_k - seq_q), (int)seq_q, (int)n_heads,
-                                          (int)n_kv_heads, 64, d_out));
+                                          (int)n_kv_heads, 64, (uint32_t*)kvs.p, (int)seq_k, d_out));
     }
     return finish(launch_sdpa_generic(nullptr, d_q, d_k, d_v, d_out, (int)seq_q, (int)seq_k, (int)n_heads,
                                       (int)n_kv_heads, (int)head_dim));

@@ -405,6 +405,19 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
 // 2^-8 before the split (power-of-two scalings, undone exactly in the
 // scores and the output), so hi overflows only for |x| >= 2^23.
 //
+// The operands are split once per layer, before the attention, by
+// kv_split_kernel into a workspace of 32-bit words (two halves each), with
+// one 64-position tile of a kv head g as 16 KB in one piece:
+//   K: word (g KP + pos) 64 + w: w < 32 the hi halves of dims 2w, 2w + 1,
+//      w >= 32 the lo halves of dims 2 (w - 32), +1;
+//   V: word ((g KT + tile) 64 + dim) 64 + w: hi (w < 32) or lo halves of
+//      the tile's keys at slots 2 w', 2 w' + 1 (w' = w mod 32), in the slot
+//      order of the P.V operands below;
+// KP = 64 KT is the key capacity rounded up to a tile; positions past the
+// last key of the last tile hold zeros.  The attention kernel then stages
+// each tile with 16-byte copies; every query tile of the same kv head reads
+// the same split words.
+//
 // Layout: lane l supplies A[l % 16][8 (l / 16) .. +7] and
 // B[8 (l / 16) .. +7][l % 16]; result r of lane l is D[4 (l / 16) + r][l % 16].
 // Scores are formed transposed as in attn_prefill_kernel (S^T = K Q^T, key
@@ -423,18 +436,9 @@ constexpr float kLoUp = 2048.0f;            // 2^11
 constexpr float kLoDown = 1.0f / 2048.0f;   // 2^-11
 constexpr float kPre = 1.0f / 256.0f;       // 2^-8 on q, k and v
 
-// hi and lo of two values, each pair packed into 32 bits
-__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-    const as_v2f v = {a * kPre, b * kPre};
-    const as_v2h h = __builtin_convertvector(v, as_v2h);
-    const as_v2f back = __builtin_convertvector(h, as_v2f);
-    const as_v2h l = __builtin_convertvector((v - back) * kLoUp, as_v2h);
-    hi = __builtin_bit_cast(uint32_t, h);
-    lo = __builtin_bit_cast(uint32_t, l);
-}
-// the same without the 2^-8 (probabilities)
-__device__ __forceinline__ void split2p(float a, float b, uint32_t& hi, uint32_t& lo) {
-    const as_v2f v = {a, b};
+// hi and lo of two values scaled by `pre`, each pair packed into 32 bits
+__device__ __forceinline__ void split2(float a, float b, float pre, uint32_t& hi, uint32_t& lo) {
+    const as_v2f v = {a * pre, b * pre};
     const as_v2h h = __builtin_convertvector(v, as_v2h);
     const as_v2f back = __builtin_convertvector(h, as_v2f);
     const as_v2h l = __builtin_convertvector((v - back) * kLoUp, as_v2h);
@@ -451,9 +455,53 @@ __device__ __forceinline__ int v_slot(int kk) {
     return 32 * u + 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3);
 }
 
+// One (64-position tile, kv head) of a layer's K and V rows into the split
+// workspace (layout above); grid (tiles, kv heads), 256 threads.  Thread t
+// splits K units e = t + 256 i (row e / 16, dims 4 (e % 16) ..) and V key
+// pairs (keys 2 p, 2 p + 1, p = e % 32, dims 4 (e / 32) ..), e = t + 256 i.
+__global__ __launch_bounds__(256) void kv_split_kernel(const float* __restrict__ kc, const float* __restrict__ vc,
+                                                       int n_keys, int kv_dim, int key_cap,
+                                                       uint32_t* __restrict__ kvs) {
+    const int tile = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int n_kv = gridDim.y;
+    const int k0 = tile * PT;
+    uint32_t* const ks = kvs + ((size_t)g * key_cap + k0) * 64;
+    uint32_t* const vs = kvs + (size_t)n_kv * key_cap * 64 + ((size_t)g * (key_cap / PT) + tile) * 64 * 64;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
+        am_v4f x = {0.f, 0.f, 0.f, 0.f};
+        if (k0 + r < n_keys) x = *(const am_v4f*)(kc + (size_t)(k0 + r) * kv_dim + g * HD + 4 * c4);
+        uint32_t h0, l0, h1, l1;
+        split2(x[0], x[1], kPre, h0, l0);
+        split2(x[2], x[3], kPre, h1, l1);
+        *(uint2*)(ks + r * 64 + 2 * c4) = make_uint2(h0, h1);
+        *(uint2*)(ks + r * 64 + 32 + 2 * c4) = make_uint2(l0, l1);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int e = tid + 256 * i, p = e & 31, c4 = e >> 5;
+        am_v4f x[2];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            x[s] = am_v4f{0.f, 0.f, 0.f, 0.f};
+            if (k0 + 2 * p + s < n_keys)
+                x[s] = *(const am_v4f*)(vc + (size_t)(k0 + 2 * p + s) * kv_dim + g * HD + 4 * c4);
+        }
+        const int w = v_slot(2 * p) >> 1;
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            uint32_t hv, lv;
+            split2(x[0][d], x[1][d], kPre, hv, lv);
+            vs[(4 * c4 + d) * 64 + w] = hv;
+            vs[(4 * c4 + d) * 64 + 32 + w] = lv;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float* __restrict__ q,
-                                                                  const float* __restrict__ kc,
-                                                                  const float* __restrict__ vc, int pos0,
+                                                                  const uint32_t* __restrict__ kvs,
+                                                                  int key_cap, int pos0,
                                                                   int m_rows, int n_heads, int n_kv_heads,
                                                                   float* __restrict__ out,
                                                                   int8_t* __restrict__ act_q,
@@ -473,9 +521,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
     const int t0 = ty * PT;
     const int g = h / (n_heads / n_kv_heads);
     const int q_dim = n_heads * HD;
-    const int kv_dim = n_kv_heads * HD;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lk = lane >> 4;
+    const uint32_t* const ks = kvs + (size_t)g * key_cap * 64;
+    const uint32_t* const vs = kvs + (size_t)n_kv_heads * key_cap * 64 + (size_t)g * key_cap * 64;
     // base-2 scores of the 2^-8-scaled operands: s' = (q . k) 2^16 scale log2(e)
     const float scale2 = (1.0f / sqrtf((float)HD)) * 1.44269504088896341f * 65536.0f;
 
@@ -494,7 +543,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
         }
         uint32_t hi[4], lo[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) split2(x[2 * j], x[2 * j + 1], hi[j], lo[j]);
+        for (int j = 0; j < 4; j++) split2(x[2 * j], x[2 * j + 1], kPre, hi[j], lo[j]);
         qh[c] = pack8(hi[0], hi[1], hi[2], hi[3]);
         ql[c] = pack8(lo[0], lo[1], lo[2], lo[3]);
     }
@@ -510,53 +559,35 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
     const int limit = pos0 + tq;
     const int unmasked_end = pos0 + t0 + 1;
 
-    // Staging.  K: this thread's four 16-byte units (row e / 16, dims
-    // 4 (e % 16) ..) for e = tid + 256 i.  V: two key pairs (keys 2 p, 2 p + 1
-    // with p = e % 32, dims 4 (e / 32) ..) for e = tid + 256 i, i < 2, so that
-    // each dim's two halves go to adjacent slots (keys 2 p and 2 p + 1 differ
-    // in their slot's last bit) as one 32-bit write.  Rows past the last key
-    // read the last key (finite values; their probabilities are zero).
-    am_v4f kreg[4], vreg[4];
+    // Staging: a tile's K (V) split words are 16 KB in one piece; thread t
+    // copies its 16-byte units e = t + 256 i, i < 4 (row e / 16, unit e % 16:
+    // units 0-7 hi halves, 8-15 lo halves) through registers into the LDS
+    // rows.  A tile's loads are issued half an iteration before it is staged
+    // (K during the softmax and P.V, V during the next scores).
+    typedef uint32_t as_u4 __attribute__((ext_vector_type(4)));
+    as_u4 kreg[4], vreg[4];
     auto load_k = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
-            kreg[i] = *(const am_v4f*)(kc + (size_t)min(kb + r, n_keys - 1) * kv_dim + g * HD + 4 * c4);
-        }
+        for (int i = 0; i < 4; i++) kreg[i] = *(const as_u4*)(ks + (size_t)kb * 64 + 4 * (tid + 256 * i));
     };
     auto load_v = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int e = tid + 256 * i, p = e & 31, c4 = e >> 5;
-#pragma unroll
-            for (int s = 0; s < 2; s++)
-                vreg[2 * i + s] =
-                    *(const am_v4f*)(vc + (size_t)min(kb + 2 * p + s, n_keys - 1) * kv_dim + g * HD + 4 * c4);
-        }
+        for (int i = 0; i < 4; i++) vreg[i] = *(const as_u4*)(vs + (size_t)kb * 64 + 4 * (tid + 256 * i));
     };
     auto store_k = [&]() {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int e = tid + 256 * i, r = e >> 4, c4 = e & 15;
-            uint32_t h0, l0, h1, l1;
-            split2(kreg[i][0], kreg[i][1], h0, l0);
-            split2(kreg[i][2], kreg[i][3], h1, l1);
-            *(uint2*)&s_kh[r][4 * c4] = make_uint2(h0, h1);
-            *(uint2*)&s_kl[r][4 * c4] = make_uint2(l0, l1);
+            const int e = tid + 256 * i, r = e >> 4, u = e & 15;
+            _Float16* const row = (u < 8) ? s_kh[r] : s_kl[r];
+            *(as_u4*)(row + 8 * (u & 7)) = kreg[i];
         }
     };
-    auto store_v = [&]() {  // transposed, keys in slot order
+    auto store_v = [&]() {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int e = tid + 256 * i, p = e & 31, c4 = e >> 5;
-            const int slot = v_slot(2 * p);
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                uint32_t hv, lv;
-                split2(vreg[2 * i][d], vreg[2 * i + 1][d], hv, lv);
-                *(uint32_t*)&s_vh[4 * c4 + d][slot] = hv;
-                *(uint32_t*)&s_vl[4 * c4 + d][slot] = lv;
-            }
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i, r = e >> 4, u = e & 15;
+            _Float16* const row = (u < 8) ? s_vh[r] : s_vl[r];
+            *(as_u4*)(row + 8 * (u & 7)) = vreg[i];
         }
     };
     load_k(0);
@@ -623,10 +654,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             uint32_t hi[4], lo[4];
-            split2p(sc[2 * u][0], sc[2 * u][1], hi[0], lo[0]);
-            split2p(sc[2 * u][2], sc[2 * u][3], hi[1], lo[1]);
-            split2p(sc[2 * u + 1][0], sc[2 * u + 1][1], hi[2], lo[2]);
-            split2p(sc[2 * u + 1][2], sc[2 * u + 1][3], hi[3], lo[3]);
+            split2(sc[2 * u][0], sc[2 * u][1], 1.0f, hi[0], lo[0]);
+            split2(sc[2 * u][2], sc[2 * u][3], 1.0f, hi[1], lo[1]);
+            split2(sc[2 * u + 1][0], sc[2 * u + 1][1], 1.0f, hi[2], lo[2]);
+            split2(sc[2 * u + 1][2], sc[2 * u + 1][3], 1.0f, hi[3], lo[3]);
             ph[u] = pack8(hi[0], hi[1], hi[2], hi[3]);
             pl[u] = pack8(lo[0], lo[1], lo[2], lo[3]);
         }
@@ -764,17 +795,30 @@ int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const
     return check_launch("attn_decode");
 }
 
+size_t attn_split_words(int max_keys, int n_kv_heads) {
+    const size_t cap = ((size_t)max_keys + PT - 1) / PT * PT;
+    return 2 * (size_t)n_kv_heads * cap * 64;
+}
+
 int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, const float* vcache, int pos0,
-                        int m, int n_heads, int n_kv_heads, int head_dim, float* out, int8_t* act_q,
-                        uint16_t* act_d) {
+                        int m, int n_heads, int n_kv_heads, int head_dim, uint32_t* kv_split, int max_keys,
+                        float* out, int8_t* act_q, uint16_t* act_d) {
     if (head_dim != HD) return set_error(SQ_ERR_UNSUPPORTED, "attention kernels are built for head_dim 64");
+    const int n_keys = pos0 + m;
+    if (n_keys > max_keys) return set_error(SQ_ERR_SHAPE, "attn_prefill: keys beyond the split workspace");
     dim3 grid(n_heads, (m + PT - 1) / PT);
-    if (attn_f32_pinned())
+    if (attn_f32_pinned()) {
         hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos0, m, n_heads,
                            n_kv_heads, out, act_q, act_d);
-    else
-        hipLaunchKernelGGL(attn_prefill_split_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos0, m, n_heads,
-                           n_kv_heads, out, act_q, act_d);
+        return check_launch("attn_prefill");
+    }
+    const int key_cap = (max_keys + PT - 1) / PT * PT;
+    hipLaunchKernelGGL(kv_split_kernel, dim3((n_keys + PT - 1) / PT, n_kv_heads), dim3(256), 0, s, kcache, vcache,
+                       n_keys, n_kv_heads * HD, key_cap, kv_split);
+    int st = check_launch("kv_split");
+    if (st) return st;
+    hipLaunchKernelGGL(attn_prefill_split_kernel, grid, dim3(256), 0, s, q, kv_split, key_cap, pos0, m, n_heads,
+                       n_kv_heads, out, act_q, act_d);
     return check_launch("attn_prefill");
 }
 

@@ -77,8 +77,13 @@ int launch_attn_decode(hipStream_t s, const float* q, const float* kcache, const
 // Writes the rows to out and/or, when act_q is non-null, their Q8_0 blocks
 // ([m][n_heads*64] and [m][n_heads*2]: what launch_quantize_rows makes of
 // out, bit for bit); either may be null.
+// kv_split: attn_split_words(max_keys, n_kv_heads) words of workspace, into
+// which the layer's K and V rows are split (f16 halves) before the
+// attention; pos0 + m may not exceed max_keys.
+size_t attn_split_words(int max_keys, int n_kv_heads);
 int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, const float* vcache,
                         int pos0, int m, int n_heads, int n_kv_heads, int head_dim,
+                        uint32_t* kv_split, int max_keys,
                         float* out, int8_t* act_q = nullptr, uint16_t* act_d = nullptr);
 // Any head_dim: one wavefront per (query, head) row; op-level entry point.
 int launch_sdpa_generic(hipStream_t s, const float* q, const float* k, const float* v, float* out,

@@ -406,6 +406,7 @@ int ensure_prefill(sq_ctx* c, size_t n) {
         (st = dmalloc(&c->p_ad, n * wmax / 32)))
         return st;
     if (!c->p_split && (st = dmalloc(&c->p_split, kPrefillSplitFloats))) return st;
+    if (!c->p_kvs && (st = dmalloc(&c->p_kvs, attn_split_words((int)c->max_pos, g.n_kv_heads)))) return st;
     c->cap_rows = n;
     return 0;
 }
@@ -660,8 +661,9 @@ int run_prefill(sq_ctx* c, size_t n) {
         // the integer path takes the attention rows as Q8_0 blocks, formed by
         // the attention kernel itself (the f32 rows are not stored)
         if ((st = phase(1)) ||
-            (st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd,
-                                      a8 ? nullptr : c->p_attn, a8 ? c->p_aq : nullptr, a8 ? c->p_ad : nullptr)) ||
+            (st = launch_attn_prefill(s, c->p_q, kc, vc, pos0, N, g.n_heads, g.n_kv_heads, hd, c->p_kvs,
+                                      (int)c->max_pos, a8 ? nullptr : c->p_attn, a8 ? c->p_aq : nullptr,
+                                      a8 ? c->p_ad : nullptr)) ||
             (st = phase(2)))
             return st;
         if (a8 && (st = tap(l, 1, QD))) return st;
@@ -939,7 +941,7 @@ void ctx_destroy(sq_ctx* c) {
     dfree(c->part_l); dfree(c->part_o); dfree(c->attn_counters); dfree(c->pv); dfree(c->pi); dfree(c->pn); dfree(c->dbg_normed);
     dfree(c->last_hidden); dfree(c->head_qs); dfree(c->head_d);
     dfree(c->p_hidden); dfree(c->p_normed); dfree(c->p_qkv); dfree(c->p_q); dfree(c->p_attn); dfree(c->p_gu);
-    dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad); dfree(c->p_split);
+    dfree(c->p_kvs); dfree(c->p_act); dfree(c->p_aq); dfree(c->p_ad); dfree(c->p_split);
     dfree(c->d_layers); dfree(c->s_stream); dfree(c->s_xchg); dfree(c->s_epoch); dfree(c->s_error); dfree(c->s_trace);
     dfree(c->d_sids); dfree(c->d_logp); dfree(c->d_id_error);
     if (c->h_pinned) (void)hipHostFree(c->h_pinned);

@@ -118,6 +118,7 @@ struct sq_ctx {
     int8_t* p_aq = nullptr;
     uint16_t* p_ad = nullptr;
     float* p_split = nullptr;  // partial tiles of a K-split prefill matmul (kPrefillSplitFloats)
+    uint32_t* p_kvs = nullptr;  // one layer's K and V split into f16 halves (attn_split_words(max_pos))
 
     // persistent decode step (one launch per token)
     bool persist = false;
