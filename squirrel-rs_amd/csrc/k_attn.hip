@@ -431,7 +431,14 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
 typedef _Float16 as_v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 as_v2h __attribute__((ext_vector_type(2)));
 typedef float as_v2f __attribute__((ext_vector_type(2)));
-constexpr int SLD = HD + 8;                 // padded LDS row (halves): 144 bytes
+// 16-byte unit swizzle of LDS row r (only bits 0-3 of r count: an operand
+// read starts at a row that is a multiple of 16): rows of one parity take eight distinct
+// values over r / 2, and rows 0-7 (8-15) of one parity four values that
+// differ from each other in bits 0 and 2, so lanes that read one unit of 16
+// consecutive rows, or units two apart of 8 rows, hit distinct banks.
+__device__ __forceinline__ int att_swz(int r) {
+    return ((r >> 1) & 1) | (((r >> 2) & 1) << 2) | (((r >> 3) & 1) << 1);
+}
 constexpr float kLoUp = 2048.0f;            // 2^11
 constexpr float kLoDown = 1.0f / 2048.0f;   // 2^-11
 constexpr float kPre = 1.0f / 256.0f;       // 2^-8 on q, k and v
@@ -506,10 +513,19 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
                                                                   float* __restrict__ out,
                                                                   int8_t* __restrict__ act_q,
                                                                   uint16_t* __restrict__ act_d) {
-    __shared__ __attribute__((aligned(16))) _Float16 s_kh[PT][SLD];  // [key][dim]
-    __shared__ __attribute__((aligned(16))) _Float16 s_kl[PT][SLD];
-    __shared__ __attribute__((aligned(16))) _Float16 s_vh[HD][SLD];  // [dim][key slot]
-    __shared__ __attribute__((aligned(16))) _Float16 s_vl[HD][SLD];
+    // K [key][dim] and V^T [dim][key slot], hi and lo halves, 128-byte rows
+    // of eight 16-byte units.  Row r keeps logical unit u at physical unit
+    // u ^ att_swz(r): the operand reads (16 rows 16 t + l % 16, one unit per
+    // lane group l / 16) then fall in distinct banks.  Each lo array starts
+    // 128 bytes past a multiple of 256 from its hi array, so that the 16
+    // lanes of a staging store (8 on a hi row, 8 on the same lo row) also do.
+    typedef _Float16 Row[HD];
+    constexpr int ARR = PT * HD, LO = ARR + 64;  // halves
+    __shared__ __attribute__((aligned(16))) _Float16 s_buf[2 * (LO + ARR)];
+    Row* const s_kh = (Row*)s_buf;
+    Row* const s_kl = (Row*)(s_buf + LO);
+    Row* const s_vh = (Row*)(s_buf + LO + ARR);
+    Row* const s_vl = (Row*)(s_buf + 2 * LO + ARR);
 
     const int h = blockIdx.x;
     // query tiles in the order of attn_prefill_kernel (equal causal work per CU)
@@ -579,7 +595,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e >> 4, u = e & 15;
             _Float16* const row = (u < 8) ? s_kh[r] : s_kl[r];
-            *(as_u4*)(row + 8 * (u & 7)) = kreg[i];
+            *(as_u4*)(row + 8 * ((u & 7) ^ att_swz(r))) = kreg[i];
         }
     };
     auto store_v = [&]() {
@@ -587,7 +603,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i, r = e >> 4, u = e & 15;
             _Float16* const row = (u < 8) ? s_vh[r] : s_vl[r];
-            *(as_u4*)(row + 8 * (u & 7)) = vreg[i];
+            *(as_u4*)(row + 8 * ((u & 7) ^ att_swz(r))) = vreg[i];
         }
     };
     load_k(0);
@@ -604,8 +620,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
             am_v4f hh = {0.f, 0.f, 0.f, 0.f}, xx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 2; c++) {
-                const as_v8h kh = *(const as_v8h*)&s_kh[16 * t + li][32 * c + 8 * lk];
-                const as_v8h kl = *(const as_v8h*)&s_kl[16 * t + li][32 * c + 8 * lk];
+                const int pu = 8 * ((4 * c + lk) ^ att_swz(li));
+                const as_v8h kh = *(const as_v8h*)&s_kh[16 * t + li][pu];
+                const as_v8h kl = *(const as_v8h*)&s_kl[16 * t + li][pu];
                 hh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], hh, 0, 0, 0);
                 xx = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], xx, 0, 0, 0);
                 xx = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[c], xx, 0, 0, 0);
@@ -668,8 +685,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
             am_v4f ah = oh[dt] * alpha, ax = ox[dt] * alpha;
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const as_v8h vh = *(const as_v8h*)&s_vh[16 * dt + li][32 * u + 8 * lk];
-                const as_v8h vl = *(const as_v8h*)&s_vl[16 * dt + li][32 * u + 8 * lk];
+                const int pu = 8 * ((4 * u + lk) ^ att_swz(li));
+                const as_v8h vh = *(const as_v8h*)&s_vh[16 * dt + li][pu];
+                const as_v8h vl = *(const as_v8h*)&s_vl[16 * dt + li][pu];
                 ah = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[u], ah, 0, 0, 0);
                 ax = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[u], ax, 0, 0, 0);
                 ax = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[u], ax, 0, 0, 0);
