@@ -431,6 +431,29 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
 typedef _Float16 as_v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 as_v2h __attribute__((ext_vector_type(2)));
 typedef float as_v2f __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) int8_t lds_i8;
+// A direct global -> LDS load (global_load_lds_dwordx4 for 16 bytes per lane,
+// global_load_lds_dword for 4): lane l reads `base + off` (base the same on
+// every lane, in SGPRs) and its bytes land at lds + SIZE * l (lds the same on
+// every lane: it goes to M0).  Issued from inline assembly, so the compiler's
+// wait-count pass does not see it; the caller waits for its loads itself
+// (s_waitcnt vmcnt) before a barrier.  M0 is named as clobbered; the compiler
+// sets M0 itself before each instruction of its own that reads it.
+template <int SIZE>
+__device__ __forceinline__ void dma_to_lds(const void* base, uint32_t off, lds_i8* lds) {
+    static_assert(SIZE == 4 || SIZE == 16, "dword or dwordx4");
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds);
+    if constexpr (SIZE == 16)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
+                     : "memory", "m0");
+}
+// s_waitcnt immediate: no vector-memory operation outstanding (the LDS and
+// export counters not waited on)
+constexpr int att_vmcnt0() { return (0x7 << 4) | (0xF << 8); }
+
 // 16-byte unit swizzle of LDS row r (only bits 0-3 of r count: an operand
 // read starts at a row that is a multiple of 16): rows of one parity take eight distinct
 // values over r / 2, and rows 0-7 (8-15) of one parity four values that
@@ -506,7 +529,7 @@ __global__ __launch_bounds__(256) void kv_split_kernel(const float* __restrict__
     }
 }
 
-__global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float* __restrict__ q,
+__global__ __launch_bounds__(256, 4) void attn_prefill_split_kernel(const float* __restrict__ q,
                                                                   const uint32_t* __restrict__ kvs,
                                                                   int key_cap, int pos0,
                                                                   int m_rows, int n_heads, int n_kv_heads,
@@ -575,41 +598,44 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
     const int limit = pos0 + tq;
     const int unmasked_end = pos0 + t0 + 1;
 
-    // Staging: a tile's K (V) split words are 16 KB in one piece; thread t
-    // copies its 16-byte units e = t + 256 i, i < 4 (row e / 16, unit e % 16:
-    // units 0-7 hi halves, 8-15 lo halves) through registers into the LDS
-    // rows.  A tile's loads are issued half an iteration before it is staged
-    // (K during the softmax and P.V, V during the next scores).
-    typedef uint32_t as_u4 __attribute__((ext_vector_type(4)));
-    as_u4 kreg[4], vreg[4];
-    auto load_k = [&](int kb) {
+    // Staging: a tile's K (V) split words are 16 KB in one piece (64 rows of
+    // 32 hi words, then 32 lo words: 256 bytes per row), copied with direct
+    // global -> LDS loads (no registers held): each 64-lane load writes 1 KB,
+    // eight 128-byte LDS rows, lane j physical unit j % 8 of row j / 8, so it
+    // reads the logical unit (j % 8) ^ att_swz(row) of that row.  Wavefront w
+    // loads rows 8 q .. 8 q + 7, q = w and w + 4, of each of the hi and lo
+    // arrays (the same lane offsets serve K and V).  A tile's loads are
+    // issued half an iteration before it is used (K during P.V, V during the
+    // next scores); each wavefront waits for its own loads, then a barrier
+    // publishes them.
+    uint32_t off[2][2];  // [hi/lo][q = w, w + 4]: byte offsets within a tile
 #pragma unroll
-        for (int i = 0; i < 4; i++) kreg[i] = *(const as_u4*)(ks + (size_t)kb * 64 + 4 * (tid + 256 * i));
-    };
-    auto load_v = [&](int kb) {
+    for (int hl = 0; hl < 2; hl++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) vreg[i] = *(const as_u4*)(vs + (size_t)kb * 64 + 4 * (tid + 256 * i));
-    };
-    auto store_k = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 256 * i, r = e >> 4, u = e & 15;
-            _Float16* const row = (u < 8) ? s_kh[r] : s_kl[r];
-            *(as_u4*)(row + 8 * ((u & 7) ^ att_swz(r))) = kreg[i];
+        for (int k = 0; k < 2; k++) {
+            const int r = 8 * (wave + 4 * k) + (lane >> 3);
+            const int u = (lane & 7) ^ att_swz(r);
+            off[hl][k] = (uint32_t)(4 * (r * 64 + 32 * hl + 4 * u));
         }
-    };
-    auto store_v = [&]() {
+    lds_i8* const lds_base = (lds_i8*)(int8_t*)s_buf;
+    lds_i8* const lk_dst[2] = {lds_base, lds_base + 2 * LO};
+    lds_i8* const lv_dst[2] = {lds_base + 2 * (LO + ARR), lds_base + 2 * (2 * LO + ARR)};
+    auto issue = [&](const uint32_t* src, lds_i8* const (&dst)[2]) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 256 * i, r = e >> 4, u = e & 15;
-            _Float16* const row = (u < 8) ? s_vh[r] : s_vl[r];
-            *(as_u4*)(row + 8 * ((u & 7) ^ att_swz(r))) = vreg[i];
-        }
+        for (int hl = 0; hl < 2; hl++)
+#pragma unroll
+            for (int k = 0; k < 2; k++) dma_to_lds<16>(src, off[hl][k], dst[hl] + 1024 * (wave + 4 * k));
     };
-    load_k(0);
-    load_v(0);
-    store_k();
-    __syncthreads();
+    auto wait_own = [] { __builtin_amdgcn_s_waitcnt(att_vmcnt0()); };
+    auto barrier = [] {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    issue(ks, lk_dst);
+    issue(vs, lv_dst);
+    wait_own();
+    barrier();
     for (int k0 = 0; k0 < n_keys; k0 += PT) {
         const bool more = k0 + PT < n_keys;
         // S^T for 4 subtiles of 16 keys: sc[t][r] = score of key k0 + 16 t + 4 lk + r
@@ -630,8 +656,6 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
 #pragma unroll
             for (int r = 0; r < 4; r++) sc[t][r] = fmaf(xx[r], kLoDown, hh[r]);
         }
-        store_v();
-        if (more) load_k(k0 + PT);
         float tmax = -INFINITY;
         if (k0 + PT > unmasked_end) {
 #pragma unroll
@@ -678,7 +702,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
             ph[u] = pack8(hi[0], hi[1], hi[2], hi[3]);
             pl[u] = pack8(lo[0], lo[1], lo[2], lo[3]);
         }
-        __syncthreads();  // V staged; every wavefront is done with s_kh / s_kl
+        wait_own();  // this wavefront's V loads
+        barrier();   // V staged; every wavefront is done with s_kh / s_kl
+        if (more) issue(ks + (size_t)(k0 + PT) * 64, lk_dst);
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
             asm volatile("" ::: "memory");
@@ -695,11 +721,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_split_kernel(const float*
             oh[dt] = ah;
             ox[dt] = ax;
         }
-        if (more) {
-            store_k();
-            load_v(k0 + PT);
-        }
-        __syncthreads();  // the next K staged; every wavefront is done with s_vh / s_vl
+        wait_own();  // this wavefront's loads of the next K
+        barrier();   // the next K staged; every wavefront is done with s_vh / s_vl
+        if (more) issue(vs + (size_t)(k0 + PT) * 64, lv_dst);
     }
     float lrow = lpart + __shfl_xor(lpart, 16, 64);
     lrow += __shfl_xor(lrow, 32, 64);
