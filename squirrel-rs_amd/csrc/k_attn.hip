@@ -450,9 +450,9 @@ __device__ __forceinline__ void dma_to_lds(const void* base, uint32_t off, lds_i
         asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
                      : "memory", "m0");
 }
-// s_waitcnt immediate: no vector-memory operation outstanding (the LDS and
-// export counters not waited on)
-constexpr int att_vmcnt0() { return (0x7 << 4) | (0xF << 8); }
+// s_waitcnt immediate: no vector-memory and no LDS operation outstanding
+// (vmcnt 0, lgkmcnt 0; the export counter not waited on)
+constexpr int att_wait_mem() { return 0x7 << 4; }
 
 // 16-byte unit swizzle of LDS row r (only bits 0-3 of r count: an operand
 // read starts at a row that is a multiple of 16): rows of one parity take eight distinct
@@ -606,8 +606,10 @@ __global__ __launch_bounds__(256, 4) void attn_prefill_split_kernel(const float*
     // loads rows 8 q .. 8 q + 7, q = w and w + 4, of each of the hi and lo
     // arrays (the same lane offsets serve K and V).  A tile's loads are
     // issued half an iteration before it is used (K during P.V, V during the
-    // next scores); each wavefront waits for its own loads, then a barrier
-    // publishes them.
+    // next scores).  Before each barrier a wavefront waits for its own loads
+    // and for its own LDS reads: the compiler may place the matrix
+    // instruction that consumes a read after the barrier, and the read must
+    // have completed before any wavefront's next loads overwrite the tile.
     uint32_t off[2][2];  // [hi/lo][q = w, w + 4]: byte offsets within a tile
 #pragma unroll
     for (int hl = 0; hl < 2; hl++)
@@ -626,7 +628,7 @@ __global__ __launch_bounds__(256, 4) void attn_prefill_split_kernel(const float*
 #pragma unroll
             for (int k = 0; k < 2; k++) dma_to_lds<16>(src, off[hl][k], dst[hl] + 1024 * (wave + 4 * k));
     };
-    auto wait_own = [] { __builtin_amdgcn_s_waitcnt(att_vmcnt0()); };
+    auto wait_own = [] { __builtin_amdgcn_s_waitcnt(att_wait_mem()); };
     auto barrier = [] {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -702,7 +704,7 @@ __global__ __launch_bounds__(256, 4) void attn_prefill_split_kernel(const float*
             ph[u] = pack8(hi[0], hi[1], hi[2], hi[3]);
             pl[u] = pack8(lo[0], lo[1], lo[2], lo[3]);
         }
-        wait_own();  // this wavefront's V loads
+        wait_own();  // this wavefront's V loads and K reads
         barrier();   // V staged; every wavefront is done with s_kh / s_kl
         if (more) issue(ks + (size_t)(k0 + PT) * 64, lk_dst);
 #pragma unroll
@@ -721,7 +723,7 @@ __global__ __launch_bounds__(256, 4) void attn_prefill_split_kernel(const float*
             oh[dt] = ah;
             ox[dt] = ax;
         }
-        wait_own();  // this wavefront's loads of the next K
+        wait_own();  // this wavefront's loads of the next K and its V reads
         barrier();   // the next K staged; every wavefront is done with s_vh / s_vl
         if (more) issue(vs + (size_t)(k0 + PT) * 64, lv_dst);
     }
