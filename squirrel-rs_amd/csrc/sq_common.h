@@ -182,11 +182,13 @@ __device__ __forceinline__ float sq_sbyte_f(int dw, int k) {
 
 typedef int sq_v4i __attribute__((ext_vector_type(4)));
 
-// sigmoid_f32 (src/kernels/sigmoid.rs:2-9) and silu_f32 (silu.rs:4-8).
+// sigmoid_f32 (src/kernels/sigmoid.rs:2-9) and silu_f32 (silu.rs:4-8):
+// x >= 0 ? 1 / (1 + exp(-x)) : exp(x) / (1 + exp(x)).  Both branches take
+// exp of -|x| (the same argument, so the same bits), formed once here; as
+// written with two branches the compiler evaluated both exponentials.
 __device__ __forceinline__ float sq_sigmoid(float x) {
-    if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
-    float z = expf(x);
-    return z / (1.0f + z);
+    const float e = expf(-fabsf(x));
+    return (x >= 0.0f ? 1.0f : e) / (1.0f + e);
 }
 
 #endif  // __HIPCC__
