@@ -253,9 +253,10 @@ def run_workload(name: str, cfg: dict, K: int, W: int, seed: int, kernel_iters: 
             block["prefill_mfma"]["attention_frac_of_f16_mfma_peak"] = round(f16_tflops / F16_MFMA_PEAK_TFLOPS, 4)
         block["prefill_roofline"] = {"bound": "mfma", "achieved": round(mm_tops, 1), "peak": INT8_PEAK_TOPS,
                                      "unit": "TOP/s", "frac": round(mm_tops / INT8_PEAK_TOPS, 4),
-                                     "kernel": "gemm_mfma32_kernel (v_mfma_i32_32x32x32_i8 on 128x128 or "
-                                               "128x64 tiles, grids of 512+) and gemm_mfma_kernel "
-                                               "(v_mfma_i32_16x16x32_i8, smaller grids, K split)"}
+                                     "kernel": "gemm_dma_kernel (v_mfma_i32_32x32x32_i8 on 128x128 tiles staged "
+                                               "by direct global-to-LDS loads; gate/up with the fused SiLU*up "
+                                               "epilogue, q|k|v, o and down with K split 2-3 ways and their "
+                                               "partial sums)"}
         log(f"[{name}] prefill phases {ph}; int8 matmul {mm_tops:.0f} TOP/s, attention {at_tflops:.1f} TFLOP/s")
     if kernel_iters and name == "q8":
         kernels = {}
