@@ -809,12 +809,19 @@ __global__ __launch_bounds__(64) void sdpa_generic_kernel(const float* q, const 
     }
 }
 
-// SQUIRREL_ATTN_F32=1 runs the prefill attention on the fp32 matrix
-// instructions (attn_prefill_kernel) instead of the split f16 ones (a test
-// and measurement aid).
-bool attn_f32_pinned() {
+// Which prefill attention runs.  Prompts whose keys fit in kF32MaxKeys take
+// attn_prefill_kernel (fp32 matrix instructions): its one small launch beats
+// the K/V split pass plus the split-f16 kernel there (32 keys: 6.6 against
+// 3.9 + 6.1 us; 128 keys: 10.8 against 4.5 + 7.6 us); longer ones take the
+// split-f16 kernel (2048 keys: 176 against 5.5 + 74 us).
+// SQUIRREL_ATTN_F32=1 pins the fp32 kernel and =0 the split one (test and
+// measurement aids).
+constexpr int kF32MaxKeys = 3 * PT;
+bool attn_use_f32(int n_keys) {
     const char* e = getenv("SQUIRREL_ATTN_F32");
-    return e && !strcmp(e, "1");
+    if (e && !strcmp(e, "1")) return true;
+    if (e && !strcmp(e, "0")) return false;
+    return n_keys <= kF32MaxKeys;
 }
 
 }  // namespace
@@ -851,7 +858,7 @@ int launch_attn_prefill(hipStream_t s, const float* q, const float* kcache, cons
     const int n_keys = pos0 + m;
     if (n_keys > max_keys) return set_error(SQ_ERR_SHAPE, "attn_prefill: keys beyond the split workspace");
     dim3 grid(n_heads, (m + PT - 1) / PT);
-    if (attn_f32_pinned()) {
+    if (attn_use_f32(n_keys)) {
         hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, s, q, kcache, vcache, pos0, m, n_heads,
                            n_kv_heads, out, act_q, act_d);
         return check_launch("attn_prefill");

@@ -156,10 +156,14 @@ def test_teacher_forced_run_in_bounds_and_matches_oracle(emu, models, wtype, mod
         assert sum(l[1] for l in lk) <= FLIP_RATE[wtype] * sum(l[0] for l in lk), lk
 
 
-def test_long_prefill_in_bounds(emu, models):
+@pytest.mark.parametrize("attn", ["auto", "split"])
+def test_long_prefill_in_bounds(emu, models, attn):
     """70 prompt rows: the unsplit matrix-core matmul tiles (m >= 64) with
-    a ragged 6-row tail, and two 64-query tiles of the prefill attention."""
-    steps, out = run(emu, [models["Q8_0"], W8A8, MULTI_KERNEL, 70, 1, 1, 128])
+    a ragged 6-row tail, and two 64-query tiles of the prefill attention
+    (the fp32 kernel the size selects, or the K/V split pass and the
+    split-f16 kernel, SQUIRREL_ATTN_F32=0)."""
+    env = {"SQUIRREL_ATTN_F32": "0"} if attn == "split" else None
+    steps, out = run(emu, [models["Q8_0"], W8A8, MULTI_KERNEL, 70, 1, 1, 128], env=env)
     assert len(steps) == 2 and all(rel <= 1e-6 and dev == ora for _, rel, _, dev, ora in steps), out
     assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
 
@@ -181,11 +185,12 @@ def test_long_prefill_fused_epilogues_in_bounds(emu, models, unfused):
     grid-size rules pick the direct-to-LDS kernel's 128 x 128 tiles for the
     FFN gate/up projection and its 128 x 64 tiles for the q|k|v projection:
     with the fused epilogues (SiLU * up with its Q8_0 blocks; RoPE and the
-    KV-cache append) and without them (SQUIRREL_PREFILL_UNFUSED=1), every
-    access stays in bounds and the logits and quantization sites match the
-    oracle."""
+    KV-cache append) and without them (SQUIRREL_PREFILL_UNFUSED=1), with the
+    attention on the K/V split pass and the split-f16 kernel
+    (SQUIRREL_ATTN_F32=0), every access stays in bounds and the logits and
+    quantization sites match the oracle."""
     steps, out = run(emu, [models["Q8_0"], W8A8, MULTI_KERNEL, 140, 1, 1, 160],
-                     env={"SQEMU_CUS": "8", "SQUIRREL_PREFILL_UNFUSED": unfused})
+                     env={"SQEMU_CUS": "8", "SQUIRREL_PREFILL_UNFUSED": unfused, "SQUIRREL_ATTN_F32": "0"})
     assert len(steps) == 2 and all(rel <= 1e-6 and dev == ora for _, rel, _, dev, ora in steps), out
     assert all(bad == 0 for _, _, _, bad, _ in locks(out)), out
 

@@ -428,7 +428,14 @@ def test_sdpa_reference_known_answers():
 
 @pytest.mark.parametrize("seq_q,seq_k", [(1, 1), (1, 37), (1, 300), (1, 4096), (200, 200), (64, 300), (5, 5)])
 @pytest.mark.parametrize("nh,nkv", [(32, 8), (8, 2), (4, 4)])
-def test_sdpa_model_kernels_match_oracle(seq_q, seq_k, nh, nkv):
+@pytest.mark.parametrize("attn", ["auto", "split"])
+def test_sdpa_model_kernels_match_oracle(seq_q, seq_k, nh, nkv, attn, monkeypatch):
+    """The model's attention kernels against the oracle: decode (one query),
+    and the prefill kernel the size selects (auto: fp32 matrix instructions
+    up to 192 keys, split-f16 beyond) or the split-f16 kernel at every size
+    (SQUIRREL_ATTN_F32=0)."""
+    if attn == "split":
+        monkeypatch.setenv("SQUIRREL_ATTN_F32", "0")
     hd = 64
     r = rng(seq_q * 1000 + seq_k + nh)
     q = r.standard_normal(seq_q * nh * hd).astype(np.float32)
@@ -457,6 +464,7 @@ def test_prefill_attention_split_f16_within_f32_noise(scale, monkeypatch):
     v = (r.standard_normal(seq_k * nkv * hd) * scale).astype(np.float32)
     st, want = O.sdpa(q, k, v, seq_q, seq_k, nh, nkv, hd)
     assert st == 0
+    monkeypatch.setenv("SQUIRREL_ATTN_F32", "0")
     got = sdpa_dev(q, k, v, seq_q, seq_k, nh, nkv, hd)
     monkeypatch.setenv("SQUIRREL_ATTN_F32", "1")
     ref = sdpa_dev(q, k, v, seq_q, seq_k, nh, nkv, hd)
@@ -467,10 +475,11 @@ def test_prefill_attention_split_f16_within_f32_noise(scale, monkeypatch):
     assert e_split <= max(4 * e_f32, 2e-6), (e_split, e_f32)
 
 
-def test_prefill_attention_large_operands():
-    """Operands up to 3e4 (beyond f16's range before the kernel's 2^-8
+def test_prefill_attention_large_operands(monkeypatch):
+    """Operands up to 3e4 (beyond f16's range before the split kernel's 2^-8
     scaling) stay finite and match the oracle: the softmax rows are then
     nearly one-hot, so the output is a v row to f32 rounding."""
+    monkeypatch.setenv("SQUIRREL_ATTN_F32", "0")
     seq_q, seq_k, nh, nkv, hd = 70, 70, 4, 4, 64
     r = rng(99)
     q = r.standard_normal(seq_q * nh * hd).astype(np.float32)
