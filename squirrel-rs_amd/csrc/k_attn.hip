@@ -415,8 +415,8 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(const float* __res
 //      order of the P.V operands below;
 // KP = 64 KT is the key capacity rounded up to a tile; positions past the
 // last key of the last tile hold zeros.  The attention kernel then stages
-// each tile with 16-byte copies; every query tile of the same kv head reads
-// the same split words.
+// each tile with direct global -> LDS loads; every query tile of the same kv
+// head reads the same split words.
 //
 // Layout: lane l supplies A[l % 16][8 (l / 16) .. +7] and
 // B[8 (l / 16) .. +7][l % 16]; result r of lane l is D[4 (l / 16) + r][l % 16].
